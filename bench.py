@@ -1,0 +1,385 @@
+"""Benchmark of the quantize / block-scaled GEMM / RoPE hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c1,c2,c3,c4,c5] [--no-cpu]
+
+Workloads are BASELINE.json's five configs, on seeded synthetic inputs:
+  c1  quantize_per_tensor_fp8 + dequantize_per_tensor_fp8, bf16 [4096, 3072]
+  c2  apply_rope (q, k) and apply_rope1 (q), bf16 [1, 24, 4608, 128], Flux freqs
+  c3  quantize_mxfp8, bf16 [4608, 3072] with per-row log-normal magnitudes   <- `value`
+  c4  scaled_mm_mxfp8, [4608, 3072] x [12288, 3072] -> bf16
+  c5  quantize_nvfp4 [8192, 5120] + scaled_mm_nvfp4 [8192, 5120] x [13824, 5120]
+
+Timing: W untimed warmup steps, then K steps captured in one HIP graph and replayed
+between HIP events on the launch stream (torch's current stream, where the ops
+launch), so Python dispatch overhead is excluded and back-to-back kernel time is
+what is measured.  Inputs/outputs rotate over buffer sets totalling > 512 MB so the
+256 MB Infinity Cache cannot hold the working set.  Graph replays are checked
+against the eager call's output before timing.
+
+Each op line reports algorithmic bytes (or FLOPs) per call / measured time, and its
+fraction of the MI355X peak (HBM 8 TB/s; dense FP8 MFMA 5.0 PF; BF16 2.5 PF).  The
+CPU baseline times the CPU oracle (a restatement of the reference eager backend) on
+a bounded sample on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "comfy-kitchen_amd", REPO):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP4_PEAK_TFLOPS = 10100.0
+ROTATE_BYTES = 512 << 20
+METRIC = "quantize GB/s (% HBM peak); scaled_mm_mxfp8 TFLOPS (% MFMA peak), 1 GPU"
+
+
+# ------------------------------------------------------------------ workloads
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def make_c1(device="cpu"):
+    """bf16 [4096, 3072], N(0,1)*0.5 with 0.1% outliers x20; scale = amax/448 (fp32)."""
+    g = gen(0)
+    x = torch.randn(4096, 3072, generator=g) * 0.5
+    n = x.numel()
+    idx = torch.randperm(n, generator=g)[: n // 1000]
+    x.view(-1)[idx] *= 20
+    x = x.bfloat16()
+    scale = (x.abs().amax().float() / 448.0).reshape(1)
+    return x.to(device), scale.to(device)
+
+
+def flux_freqs(h=72, w=64, axes=(16, 56, 56), theta=10000.0) -> torch.Tensor:
+    """Flux EmbedND rotation matrices for ids (0, i, j), i < h, j < w: [1, 1, h*w, 64, 2, 2] fp32."""
+    ii, jj = torch.meshgrid(torch.arange(h), torch.arange(w), indexing="ij")
+    ids = torch.stack([torch.zeros_like(ii), ii, jj], dim=-1).reshape(-1, 3).double()
+    mats = []
+    for a, d in enumerate(axes):
+        omega = 1.0 / theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d)
+        phi = ids[:, a:a + 1] * omega[None, :]
+        m = torch.stack([torch.cos(phi), -torch.sin(phi), torch.sin(phi), torch.cos(phi)], dim=-1)
+        mats.append(m.reshape(-1, d // 2, 2, 2))
+    return torch.cat(mats, dim=1).float().reshape(1, 1, h * w, sum(axes) // 2, 2, 2)
+
+
+def make_c2(device="cpu"):
+    g = gen(1)
+    q = torch.randn(1, 24, 4608, 128, generator=g).bfloat16()
+    k = torch.randn(1, 24, 4608, 128, generator=g).bfloat16()
+    return q.to(device), k.to(device), flux_freqs().to(device)
+
+
+def make_c3(device="cpu"):
+    g = gen(2)
+    x = torch.randn(4608, 3072, generator=g) * torch.exp(torch.randn(4608, 1, generator=g))
+    return x.bfloat16().to(device)
+
+
+def make_c4_weight(device="cpu"):
+    return (torch.randn(12288, 3072, generator=gen(3)) * 0.02).bfloat16().to(device)
+
+
+def make_c5(device="cpu"):
+    a = torch.randn(8192, 5120, generator=gen(4)).bfloat16()
+    w = (torch.randn(13824, 5120, generator=gen(5)) * 0.02).bfloat16()
+    ga = (a.abs().amax().float() / 2688.0).reshape(1)
+    gw = (w.abs().amax().float() / 2688.0).reshape(1)
+    return a.to(device), w.to(device), ga.to(device), gw.to(device)
+
+
+# Algorithmic bytes / FLOPs per call (inputs read once + outputs written once).
+BYTES = {
+    "quantize_per_tensor_fp8": 4096 * 3072 * 3 + 4,
+    "dequantize_per_tensor_fp8": 4096 * 3072 * 3 + 4,
+    "apply_rope": 4 * 24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4,
+    "apply_rope1": 2 * 24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4,
+    "quantize_mxfp8": 4608 * 3072 * 3 + 4608 * 96,
+    "quantize_nvfp4": 8192 * 5120 * 2 + 8192 * 2560 + 8192 * 320 + 4,
+}
+FLOPS = {
+    "scaled_mm_mxfp8": 2 * 4608 * 12288 * 3072,
+    "scaled_mm_nvfp4": 2 * 8192 * 13824 * 5120,
+}
+
+
+# ------------------------------------------------------------------ timing
+def _sets_for(bytes_per_set: int) -> int:
+    return max(2, math.ceil(ROTATE_BYTES / max(bytes_per_set, 1)))
+
+
+def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> float:
+    """Average ms per call: `make_call(i)` returns a zero-arg launcher for buffer set i."""
+    calls = [make_call(i) for i in range(n_sets)]
+    for i in range(warmup):
+        calls[i % n_sets]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        calls[0]()  # warm the capture stream's allocator pool
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            outs = [calls[i % n_sets]() for i in range(steps)]
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    if check is not None:
+        check(outs)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_cpu(fn, min_reps=2, budget_s=8.0) -> tuple[float, int]:
+    """Median seconds per call of fn() on the CPU (bounded by budget_s after one warmup)."""
+    fn()
+    ts = []
+    t_all = time.perf_counter()
+    while len(ts) < min_reps or (time.perf_counter() - t_all < budget_s and len(ts) < 5):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], len(ts)
+
+
+def roofline_bytes(nbytes, ms, traffic=None):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+
+
+def roofline_flops(flops, ms, peak, traffic=None):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(tf / peak, 4), "traffic": traffic}
+
+
+def load_traffic() -> dict:
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), if recorded."""
+    p = REPO / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch", {})
+        except (ValueError, OSError):
+            return {}
+    return {}
+
+
+# ------------------------------------------------------------------ runs
+def run_gpu(configs, steps, warmup, log):
+    import comfy_kitchen as ck
+
+    from oracle import eager_ref  # checker only: verifies graph replays against the oracle on a slice
+    dev = torch.device("cuda", 0)
+    res = {}
+    traffic = load_traffic()
+
+    def same(a, b):
+        return torch.equal(a.view(torch.uint8) if a.element_size() == 1 else a, b.view(torch.uint8) if b.element_size() == 1 else b)
+
+    if "c1" in configs:
+        x, scale = make_c1(dev)
+        nset = _sets_for(BYTES["quantize_per_tensor_fp8"])
+        xs = [x.clone() for _ in range(nset)]
+        ref_q = ck.quantize_per_tensor_fp8(x, scale)
+        ms = time_graph(lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps, warmup,
+                        check=lambda outs: [same(o, ref_q) or sys.exit("graph replay mismatch c1 q") for o in outs])
+        res["quantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_per_tensor_fp8"], ms,
+                                                                      traffic.get("quantize_fp8"))}
+        log(f"c1 quantize_per_tensor_fp8: {ms * 1e3:.2f} us")
+        qs = [ref_q.clone() for _ in range(nset)]
+        ref_dq = ck.dequantize_per_tensor_fp8(ref_q, scale)
+        ms = time_graph(lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
+                        check=lambda outs: [same(o, ref_dq) or sys.exit("graph replay mismatch c1 dq") for o in outs])
+        res["dequantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_per_tensor_fp8"], ms,
+                                                                        traffic.get("dequantize_fp8"))}
+        log(f"c1 dequantize_per_tensor_fp8: {ms * 1e3:.2f} us")
+        del xs, qs
+
+    if "c2" in configs:
+        q, k, f = make_c2(dev)
+        nset = _sets_for(BYTES["apply_rope"])
+        qs = [q.clone() for _ in range(nset)]
+        ks = [k.clone() for _ in range(nset)]
+        rq, rk = ck.apply_rope(q, k, f)
+        ms = time_graph(lambda i: (lambda: ck.apply_rope(qs[i], ks[i], f)), nset, steps, warmup,
+                        check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
+        res["apply_rope"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope"], ms, traffic.get("apply_rope"))}
+        log(f"c2 apply_rope: {ms * 1e3:.2f} us")
+        ms = time_graph(lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup)
+        res["apply_rope1"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope1"], ms, traffic.get("apply_rope1"))}
+        log(f"c2 apply_rope1: {ms * 1e3:.2f} us")
+        del qs, ks
+
+    if "c3" in configs or "c4" in configs:
+        x = make_c3(dev)
+        qa, sa = ck.quantize_mxfp8(x)
+        if "c3" in configs:
+            nset = _sets_for(BYTES["quantize_mxfp8"])
+            xs = [x.clone() for _ in range(nset)]
+            ms = time_graph(lambda i: (lambda: ck.quantize_mxfp8(xs[i])), nset, steps, warmup,
+                            check=lambda outs: [(same(a, qa) and same(b, sa)) or sys.exit("graph mismatch c3")
+                                                for a, b in outs])
+            res["quantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_mxfp8"], ms,
+                                                                 traffic.get("quantize_mxfp8"))}
+            log(f"c3 quantize_mxfp8: {ms * 1e3:.2f} us")
+            del xs
+        if "c4" in configs:
+            qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
+            try:
+                ref = ck.scaled_mm_mxfp8(qa, qw, sa, sw)
+                ms = time_graph(lambda i: (lambda: ck.scaled_mm_mxfp8(qa, qw, sa, sw)), 2, max(steps // 4, 5),
+                                warmup, check=lambda outs: [same(o, ref) or sys.exit("graph mismatch c4") for o in outs])
+                res["scaled_mm_mxfp8"] = {"ms": ms, **roofline_flops(FLOPS["scaled_mm_mxfp8"], ms, FP8_PEAK_TFLOPS,
+                                                                      traffic.get("scaled_mm_mxfp8"))}
+                log(f"c4 scaled_mm_mxfp8: {ms * 1e3:.1f} us")
+            except RuntimeError as e:
+                res["scaled_mm_mxfp8"] = {"error": str(e)}
+                log(f"c4 scaled_mm_mxfp8 unavailable: {e}")
+
+    if "c5" in configs:
+        a, w, ga, gw = make_c5(dev)
+        qa, sa = ck.quantize_nvfp4(a, ga)
+        nset = _sets_for(BYTES["quantize_nvfp4"])
+        as_ = [a.clone() for _ in range(nset)]
+        ms = time_graph(lambda i: (lambda: ck.quantize_nvfp4(as_[i], ga)), nset, steps, warmup,
+                        check=lambda outs: [(same(x_, qa) and same(y_, sa)) or sys.exit("graph mismatch c5")
+                                            for x_, y_ in outs])
+        res["quantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["quantize_nvfp4"], ms, traffic.get("quantize_nvfp4"))}
+        log(f"c5 quantize_nvfp4: {ms * 1e3:.2f} us")
+        del as_
+        qw, sw = ck.quantize_nvfp4(w, gw)
+        try:
+            ref = ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)
+            ms = time_graph(lambda i: (lambda: ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)), 2, max(steps // 4, 5),
+                            warmup, check=lambda outs: [same(o, ref) or sys.exit("graph mismatch c5 mm") for o in outs])
+            r = roofline_flops(FLOPS["scaled_mm_nvfp4"], ms, BF16_PEAK_TFLOPS, traffic.get("scaled_mm_nvfp4"))
+            r["frac_of_fp4_peak"] = round(r["achieved"] / FP4_PEAK_TFLOPS, 4)
+            res["scaled_mm_nvfp4"] = {"ms": ms, **r}
+            log(f"c5 scaled_mm_nvfp4: {ms * 1e3:.1f} us")
+        except RuntimeError as e:
+            res["scaled_mm_nvfp4"] = {"error": str(e)}
+            log(f"c5 scaled_mm_nvfp4 unavailable: {e}")
+    return res
+
+
+def run_cpu_baseline(configs, log):
+    """Time the CPU oracle (restatement of the reference eager path) on bounded samples."""
+    from oracle import eager_ref as ref
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    out = {}
+    if "c3" in configs:
+        x = make_c3()
+        s, reps = time_cpu(lambda: ref.quantize_mxfp8(x))
+        out["quantize_mxfp8"] = {"value": round(BYTES["quantize_mxfp8"] / s / 1e9, 3), "unit": "GB/s",
+                                 "cores": cores, "kind": "port",
+                                 "sample": f"full C3 tensor [4608, 3072] bf16, median of {reps} runs"}
+        log(f"cpu quantize_mxfp8: {s * 1e3:.1f} ms")
+    if "c1" in configs:
+        x, scale = make_c1()
+        s, reps = time_cpu(lambda: ref.quantize_per_tensor_fp8(x, scale))
+        out["quantize_per_tensor_fp8"] = {"value": round(BYTES["quantize_per_tensor_fp8"] / s / 1e9, 3),
+                                          "unit": "GB/s", "cores": cores, "kind": "port",
+                                          "sample": f"full C1 tensor, median of {reps} runs"}
+    if "c2" in configs:
+        q, k, f = make_c2()
+        s, reps = time_cpu(lambda: ref.apply_rope(q, k, f))
+        out["apply_rope"] = {"value": round(BYTES["apply_rope"] / s / 1e9, 3), "unit": "GB/s", "cores": cores,
+                             "kind": "port", "sample": f"full C2 q,k, median of {reps} runs"}
+    if "c5" in configs:
+        a = make_c5()[0][:1024]
+        ga = (a.abs().amax().float() / 2688).reshape(1)
+        s, reps = time_cpu(lambda: ref.quantize_nvfp4(a, ga))
+        out["quantize_nvfp4"] = {"value": round(BYTES["quantize_nvfp4"] / 8 / s / 1e9, 3), "unit": "GB/s",
+                                 "cores": cores, "kind": "port",
+                                 "sample": f"first 1024 of 8192 rows of C5 A, median of {reps} runs"}
+    if "c4" in configs:
+        # eager scaled_mm has no CPU kernel; stand-in: dequantize both operands, fp32 matmul
+        x = make_c3()[:512]
+        wq, ws = ref.quantize_mxfp8(make_c4_weight())
+        xq, xs = ref.quantize_mxfp8(x)
+        s, reps = time_cpu(lambda: ref.scaled_mm_mxfp8_ref(xq, wq, xs, ws), min_reps=1, budget_s=10)
+        out["scaled_mm_mxfp8"] = {"value": round(2 * 512 * 12288 * 3072 / s / 1e12, 4), "unit": "TFLOP/s",
+                                  "cores": cores, "kind": "port",
+                                  "sample": f"512 of 4608 rows of A: dequantize + fp32 matmul, median of {reps}"}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the quantizers/GEMMs shard by rows with no exchange; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+    configs = set(args.configs.split(","))
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a GPU")
+    import comfy_kitchen as ck
+
+    if not ck.list_backends()["hip"]["available"]:
+        sys.exit(f"hip backend unavailable: {ck.list_backends()['hip']['unavailable_reason']}")
+    gpu = run_gpu(configs, args.steps, args.warmup, log)
+    cpu = {} if args.no_cpu else run_cpu_baseline(configs, log)
+
+    primary = "quantize_mxfp8" if "quantize_mxfp8" in gpu else next(iter(gpu))
+    p = gpu[primary]
+    roof = {k: p[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    line = {
+        "metric": METRIC,
+        "value": p["achieved"],
+        "unit": p["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(p["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16->e4m3/e8m0",
+        "data": "synthetic (seeded; BASELINE.json config shapes and distributions)",
+        "config": {"workload": f"{primary} (BASELINE config 3: bf16 [4608, 3072], per-row log-normal)",
+                   "timing": "HIP graph of K calls, rotating >512MB of buffers, HIP events on the launch stream"},
+        "roofline": roof,
+        "cpu_baseline": cpu.get(primary),
+        "ops": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in gpu.items()},
+        "cpu_baselines": cpu,
+        "device": torch.cuda.get_device_properties(0).gcnArchName,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,83 @@
+"""Build the gfx950 C-ABI library libckh.so in-tree (no JIT, no torch extension).
+
+    python comfy-kitchen_amd/build.py            # build (always recompiles)
+
+Every csrc/*.hip file is compiled by hipcc for gfx950 only and linked into
+comfy_kitchen/backends/hip/libckh.so, which the "hip" backend loads with ctypes.
+
+Flags: -O3; no fast-math (the quantizers need IEEE division and exact rounding);
+-ffp-contract=off so no multiply-add is fused behind the kernels' back (the kernels
+call __fmaf_rn where a fused multiply-add is intended); packed-FP32 instructions are
+disabled for the device pass.  Code object v5 is used because the extension runs inside
+torch's bundled HIP runtime (same SONAME as /opt/rocm's), which may be older than hipcc.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent
+CSRC = HERE / "csrc"
+OUT = HERE / "comfy_kitchen" / "backends" / "hip" / "libckh.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-mcode-object-version=5",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-gpu-rdc",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{REPO / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(cand).exists():
+        raise RuntimeError("hipcc not found; ROCm is required to build libckh.so")
+    return cand
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> Path:
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    objs = [objdir / (s.stem + ".o") for s in sources]
+    workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 8)
+    with cf.ThreadPoolExecutor(max_workers=max(workers, 1)) as ex:
+        list(ex.map(_compile, sources, objs))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT.relative_to(REPO)} from {len(sources)} sources")
+    return OUT
+
+
+if __name__ == "__main__":
+    build()

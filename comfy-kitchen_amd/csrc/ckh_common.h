@@ -1,0 +1,193 @@
+// Shared device helpers for the gfx950 kernels: dtype codes, exact float format
+// conversions, the 32_4_4 scale swizzle, and the thread-local error channel.
+//
+// Every conversion here is written from the format definitions (IEEE-754 binary16 /
+// bfloat16, OCP FP8 E4M3FN / E5M2, OCP MX E8M0, OCP FP4 E2M1) with round-to-nearest-
+// even, so results do not depend on the FP mode register or on hardware convert
+// instructions.  Callers clamp to the finite range before FP8 encoding, as the
+// reference's eager backend does (backends/eager/quantization.py:54,154,314).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ckh.h"
+
+namespace ckh {
+
+// ------------------------------------------------------------------ errors
+void set_error(const char* fmt, ...);
+void clear_error();
+int check_launch(const char* what);
+
+#define CKH_REQUIRE(cond, ...)            \
+    do {                                  \
+        if (!(cond)) {                    \
+            ::ckh::set_error(__VA_ARGS__); \
+            return CKH_ERR_INVALID;       \
+        }                                 \
+    } while (0)
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t rup(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+
+// --------------------------------------------------------- bit reinterpret
+__device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
+
+// ------------------------------------------------------ 16-bit float formats
+// bfloat16 <-> float.  Widening is exact.  Narrowing is round-to-nearest-even; a NaN
+// becomes a quiet NaN with its sign kept.
+__device__ __forceinline__ float bf16_to_f(uint32_t h) { return as_f(h << 16); }
+__device__ __forceinline__ uint32_t f_to_bf16(float f) {
+    uint32_t u = as_u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
+
+// binary16 <-> float through the IEEE conversion instructions (round-to-nearest-even,
+// subnormals kept, which is the default FP mode of HIP kernels).
+__device__ __forceinline__ float f16_to_f(uint32_t h) {
+    _Float16 v;
+    uint16_t hb = static_cast<uint16_t>(h);
+    __builtin_memcpy(&v, &hb, 2);
+    return static_cast<float>(v);
+}
+__device__ __forceinline__ uint32_t f_to_f16(float f) {
+    _Float16 v = static_cast<_Float16>(f);
+    uint16_t hb;
+    __builtin_memcpy(&hb, &v, 2);
+    return hb;
+}
+__device__ __forceinline__ float round_f16(float f) { return f16_to_f(f_to_f16(f)); }
+
+// Round a float to the precision of dtype code `c` (f32 is the identity).
+template <int C>
+__device__ __forceinline__ float round_to(float f) {
+    if constexpr (C == CKH_BF16) return round_bf16(f);
+    else if constexpr (C == CKH_F16) return round_f16(f);
+    else return f;
+}
+
+// -------------------------------------------------------------- OCP FP8
+// E4M3FN: bias 7, 3 mantissa bits, no infinities, 0x7F/0xFF NaN, max 448.
+// Input must be in [-448, 448] or NaN.  NaN encodes as 0xFF (the all-ones NaN that
+// PyTorch's vectorised CPU clamp produces).
+__device__ __forceinline__ uint32_t f_to_e4m3(float f) {
+    uint32_t u = as_u(f);
+    uint32_t s = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0xffu;
+    uint32_t m;
+    if (a < 0x3c800000u) {  // |f| < 2^-6: subnormal codes, quantum 2^-9
+        // Adding 2^14 (whose ulp is 2^-9) rounds |f| to a multiple of 2^-9 (RNE).
+        m = as_u(as_f(a) + 16384.0f) - 0x46800000u;
+    } else {  // rebias exponent 127 -> 7, round mantissa at bit 20 to nearest even
+        m = (a - (120u << 23) + 0x7ffffu + ((a >> 20) & 1u)) >> 20;
+    }
+    return s | m;
+}
+
+// E5M2: bias 15, 2 mantissa bits, max 57344.  Input in [-57344, 57344] or NaN.
+__device__ __forceinline__ uint32_t f_to_e5m2(float f) {
+    uint32_t u = as_u(f);
+    uint32_t s = (u >> 24) & 0x80u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0xffu;
+    uint32_t m;
+    if (a < 0x38800000u) {  // |f| < 2^-14: subnormal codes, quantum 2^-16
+        m = as_u(as_f(a) + 128.0f) - 0x43000000u;
+    } else {
+        m = (a - (112u << 23) + 0xfffffu + ((a >> 21) & 1u)) >> 21;
+    }
+    return s | m;
+}
+
+__device__ __forceinline__ float e4m3_to_f(uint32_t c) {
+    uint32_t s = (c & 0x80u) << 24;
+    uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+    if ((c & 0x7fu) == 0x7fu) return as_f(s | 0x7fc00000u);
+    if (e == 0) return as_f(s | as_u(static_cast<float>(m) * 0.001953125f));  // m * 2^-9
+    return as_f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+__device__ __forceinline__ float e5m2_to_f(uint32_t c) {
+    uint32_t s = (c & 0x80u) << 24;
+    uint32_t e = (c >> 2) & 0x1fu, m = c & 3u;
+    if (e == 0x1f) return as_f(s | (m ? 0x7fc00000u : 0x7f800000u));
+    if (e == 0) return as_f(s | as_u(static_cast<float>(m) * 1.52587890625e-05f));  // m * 2^-16
+    return as_f(s | ((e + 112u) << 23) | (m << 21));
+}
+
+// --------------------------------------------------------------- OCP E8M0
+// Scale byte e -> 2^(e-127); e == 0 decodes to 0.0 (reference float_utils.py:376-382).
+__device__ __forceinline__ float e8m0_to_f(uint32_t e) { return as_f(e == 0 ? 0u : (e << 23)); }
+
+// --------------------------------------------------------------- OCP E2M1
+// Round-to-nearest-even of |v| (already clamped to [0, 6]) onto the magnitudes
+// {0, 0.5, 1, 1.5, 2, 3, 4, 6} = codes 0..7.  Each threshold is the midpoint between
+// neighbouring magnitudes; at a midpoint the even code wins, hence > or >=.
+__device__ __forceinline__ uint32_t e2m1_mag(float a) {
+    return (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) +
+           (a > 5.0f);
+}
+__device__ __forceinline__ uint32_t f_to_e2m1(float v) {
+    return ((as_u(v) >> 28) & 8u) | e2m1_mag(fabsf(v));
+}
+// Code -> value (sign in bit 3).
+__device__ __forceinline__ float e2m1_to_f(uint32_t c) {
+    // Codes 2..7 are normal: exponent (mag >> 1) - 1, one mantissa bit (mag & 1).
+    const uint32_t mag = c & 7u;
+    uint32_t bits = mag >= 2u ? (((126u + (mag >> 1)) << 23) | ((mag & 1u) << 22))
+                              : (mag ? 0x3f000000u : 0u);
+    return as_f(bits | ((c & 8u) << 28));
+}
+
+// -------------------------------------------------------- 32_4_4 swizzle
+// Byte offset of logical scale (r, c) in a swizzled tensor whose logical width is
+// C (n_cb = ceil(C/4) column blocks).  4 consecutive c (4j..4j+3) of one row are one
+// aligned 32-bit word.
+__host__ __device__ __forceinline__ int64_t swz_offset(int64_t r, int64_t c, int64_t n_cb) {
+    return (((r >> 7) * n_cb + (c >> 2)) * 32 + (r & 31)) * 16 + ((r & 127) >> 5) * 4 + (c & 3);
+}
+
+// ---------------------------------------------------------- element loads
+// Load 8 consecutive elements of dtype code C as floats from an address aligned to
+// 8 * sizeof(element).
+template <int C>
+__device__ __forceinline__ void load8(const void* p, float (&v)[8]) {
+    if constexpr (C == CKH_F32) {
+        const float4* q = reinterpret_cast<const float4*>(p);
+        float4 a = q[0], b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        uint4 w = *reinterpret_cast<const uint4*>(p);
+        uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (C == CKH_BF16) {
+                v[2 * i] = bf16_to_f(d[i] & 0xffffu);
+                v[2 * i + 1] = bf16_to_f(d[i] >> 16);
+            } else {
+                v[2 * i] = f16_to_f(d[i] & 0xffffu);
+                v[2 * i + 1] = f16_to_f(d[i] >> 16);
+            }
+        }
+    }
+}
+
+// Load one element of dtype code C as float.
+template <int C>
+__device__ __forceinline__ float load1(const void* p, int64_t i) {
+    if constexpr (C == CKH_F32) return reinterpret_cast<const float*>(p)[i];
+    else if constexpr (C == CKH_BF16) return bf16_to_f(reinterpret_cast<const uint16_t*>(p)[i]);
+    else return f16_to_f(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+template <int C>
+struct ElemSize { static constexpr int value = (C == CKH_F32) ? 4 : 2; };
+
+}  // namespace ckh

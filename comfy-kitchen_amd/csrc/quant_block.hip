@@ -1,0 +1,356 @@
+// Block-scaled quantizers (MXFP8, NVFP4) and their dequantizers for gfx950.
+//
+// Work unit: one row r and one group of four consecutive K-blocks (the four blocks
+// whose scales form one aligned 32-bit word of the 32_4_4 swizzled layout).  Lanes of
+// a unit each load 8 consecutive input elements (one 16-byte load for 16-bit inputs),
+// so a wavefront reads a contiguous row segment; the block amax is reduced across the
+// lanes of the block, and the four scale bytes are OR-combined across the unit so that
+// one lane writes the scale word with a single 32-bit store.  Units cover the padded
+// scale rows (a multiple of 128) so the kernel also writes every padding byte: outputs
+// can be allocated uninitialised.
+//
+//   MXFP8: 32-element blocks, 4 lanes per block, 16 lanes per unit.
+//   NVFP4: 16-element blocks, 2 lanes per block,  8 lanes per unit.
+#include "ckh_common.h"
+
+namespace ckh {
+
+constexpr int kThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int m) {
+    return __shfl_xor(v, m, 64);
+}
+
+// Load the 8 elements [k0, k0+8) of row r of x [orows, ocols]; outside x they are 0
+// (the zero padding of pad_32x / pad_16x).
+template <int IN>
+__device__ __forceinline__ void load_row8(const void* x, int64_t r, int64_t k0, int64_t orows, int64_t ocols,
+                                          bool vec_ok, float (&v)[8]) {
+    constexpr int ES = ElemSize<IN>::value;
+    if (vec_ok && r < orows && k0 + 8 <= ocols) {
+        load8<IN>(static_cast<const char*>(x) + (r * ocols + k0) * ES, v);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = (r < orows && k0 + t < ocols) ? load1<IN>(x, r * ocols + k0 + t) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ uint32_t absmax_bits(const float (&v)[8]) {
+    // |v| as integers orders like the floats (NaN above +inf), so an integer max is
+    // the float amax, NaN-propagating like torch.amax.
+    uint32_t m = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) m = max(m, as_u(v[t]) & 0x7fffffffu);
+    return m;
+}
+
+// ------------------------------------------------------------------- MXFP8
+// E8M0 exponent of a block from its amax bits (reference eager quantization.py:292-302):
+//   s = max(amax/448, 2^-127); e = clamp(ceil(log2 s) + 127, 0, 254).
+// ceil(log2 s) is taken exactly from the bit fields of s: for normal s it is the
+// unbiased exponent plus one if any mantissa bit is set; s = 2^-127 (the clamp) gives
+// e = 0 and the only other subnormals, 2^-127 < s < 2^-126, give e = 1.  Non-finite
+// amax gives e = 0, as the reference's float->int32 conversion of ceil(log2(inf/NaN))
+// does on x86.
+__device__ __forceinline__ uint32_t mx_exponent(uint32_t amax_bits) {
+    if (amax_bits == 0 || amax_bits >= 0x7f800000u) return 0;
+    uint32_t s = as_u(as_f(amax_bits) / 448.0f);
+    if (s <= 0x00400000u) return 0;
+    if (s < 0x00800000u) return 1;
+    uint32_t e = (s >> 23) + ((s & 0x7fffffu) != 0);
+    return e > 254u ? 254u : e;
+}
+
+// Codes for one lane's 8 values given the block's amax bits and exponent.
+__device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_bits, uint32_t e) {
+    uint32_t w[2] = {0u, 0u};
+    if (amax_bits == 0) return make_uint2(0u, 0u);  // zero block: +0 codes
+    if (e == 0) {
+        // Scale 0.0: x/0 is +-inf (clamped to +-448) for x != 0 and NaN for x == 0.
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t a = as_u(v[t]) & 0x7fffffffu;
+            uint32_t c = (a == 0 || a > 0x7f800000u) ? 0xffu : (0x7eu | ((as_u(v[t]) >> 24) & 0x80u));
+            w[t >> 2] |= c << (8 * (t & 3));
+        }
+        return make_uint2(w[0], w[1]);
+    }
+    // x / 2^(e-127) == x * 2^(127-e) exactly (both correctly rounded); 1 <= e <= 254
+    // keeps 2^(127-e) a normal float.
+    const float mul = as_f((254u - e) << 23);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        float q = v[t] * mul;
+        q = q > 448.0f ? 448.0f : (q < -448.0f ? -448.0f : q);
+        w[t >> 2] |= f_to_e4m3(q) << (8 * (t & 3));
+    }
+    return make_uint2(w[0], w[1]);
+}
+
+template <int IN>
+__global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __restrict__ x,
+                                                                  uint8_t* __restrict__ qx,
+                                                                  uint32_t* __restrict__ sc, int64_t rows,
+                                                                  int64_t cols, int64_t orows, int64_t ocols,
+                                                                  int64_t n_cb, int64_t n_units, bool vec_ok) {
+    const int64_t unit = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 4;
+    if (unit >= n_units) return;  // whole 16-lane units leave together
+    const int l = threadIdx.x & 15;
+    const int64_t r = unit / n_cb;
+    const int64_t j = unit - r * n_cb;
+    const int64_t blk = 4 * j + (l >> 2);
+    const int64_t k0 = blk * 32 + (l & 3) * 8;
+    const bool live = r < rows && blk < cols / 32;
+
+    float v[8];
+    load_row8<IN>(x, r, k0, orows, ocols, vec_ok, v);
+    uint32_t m = absmax_bits(v);
+    m = max(m, shfl_xor(m, 1));
+    m = max(m, shfl_xor(m, 2));
+    const uint32_t e = live ? mx_exponent(m) : 0u;
+
+    if (live) *reinterpret_cast<uint2*>(qx + r * cols + k0) = mx_encode8(v, m, e);
+
+    uint32_t word = e << (8 * (l >> 2));
+    word |= shfl_xor(word, 4);
+    word |= shfl_xor(word, 8);
+    if (l == 0) sc[swz_offset(r, 4 * j, n_cb) >> 2] = word;
+}
+
+// ------------------------------------------------------------------- NVFP4
+// Per 16-element block (reference eager quantization.py:137-158):
+//   s8 = E4M3(min(amax/6/g, 448)); T = g*s8; codes = E2M1(clamp(x/T, +-6)), T==0 -> +0.
+// Divisions are IEEE fp32 divisions, as in the reference's eager path.
+template <int IN>
+__global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __restrict__ x,
+                                                                  const float* __restrict__ gptr,
+                                                                  uint8_t* __restrict__ qx,
+                                                                  uint32_t* __restrict__ sc, int64_t rows,
+                                                                  int64_t cols, int64_t orows, int64_t ocols,
+                                                                  int64_t n_cb, int64_t n_units, bool vec_ok,
+                                                                  bool hi_first) {
+    const int64_t unit = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
+    if (unit >= n_units) return;  // whole 8-lane units leave together
+    const int l = threadIdx.x & 7;
+    const int64_t r = unit / n_cb;
+    const int64_t j = unit - r * n_cb;
+    const int64_t blk = 4 * j + (l >> 1);
+    const int64_t k0 = blk * 16 + (l & 1) * 8;
+    const bool live = r < rows && blk < cols / 16;
+    const float g = gptr[0];
+
+    float v[8];
+    load_row8<IN>(x, r, k0, orows, ocols, vec_ok, v);
+    uint32_t m = absmax_bits(v);
+    m = max(m, shfl_xor(m, 1));
+
+    float c = (as_f(m) / 6.0f) / g;
+    c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
+    const uint32_t s8 = live ? f_to_e4m3(c) : 0u;
+    const float T = g * e4m3_to_f(s8);
+
+    if (live) {
+        uint32_t codes[8];
+        if (T == 0.0f) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) codes[t] = 0;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                float q = v[t] / T;
+                q = q > 6.0f ? 6.0f : (q < -6.0f ? -6.0f : q);
+                codes[t] = f_to_e2m1(q);
+            }
+        }
+        uint32_t w = 0;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            uint32_t b = hi_first ? ((codes[2 * p] << 4) | codes[2 * p + 1]) : ((codes[2 * p + 1] << 4) | codes[2 * p]);
+            w |= b << (8 * p);
+        }
+        *reinterpret_cast<uint32_t*>(qx + r * (cols / 2) + k0 / 2) = w;
+    }
+
+    uint32_t word = s8 << (8 * (l >> 1));
+    word |= shfl_xor(word, 2);
+    word |= shfl_xor(word, 4);
+    if (l == 0) sc[swz_offset(r, 4 * j, n_cb) >> 2] = word;
+}
+
+// -------------------------------------------------------------- dequantize
+template <int OUT>
+__device__ __forceinline__ void store8(void* out, int64_t i, const float (&v)[8]) {
+    if constexpr (OUT == CKH_F32) {
+        float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+        p[0] = make_float4(v[0], v[1], v[2], v[3]);
+        p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16(v[2 * q]) : f_to_f16(v[2 * q]);
+            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
+            w[q] = lo | (hi << 16);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// MXFP8 dequantize (reference eager quantization.py:342-364):
+//   out = (float(q) * 2^(e-127)).to(out), e == 0 -> scale 0.0.
+// One thread per 8 elements of one 32-block.
+template <int OUT>
+__global__ __launch_bounds__(kThreads) void dequantize_mxfp8_kernel(const uint8_t* __restrict__ qx,
+                                                                    const uint8_t* __restrict__ sc,
+                                                                    void* __restrict__ out, int64_t rows,
+                                                                    int64_t cols, int64_t n_cb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t per_row = cols / 8;
+    if (t >= rows * per_row) return;
+    const int64_t r = t / per_row;
+    const int64_t k0 = (t - r * per_row) * 8;
+    const float s = e8m0_to_f(sc[swz_offset(r, k0 / 32, n_cb)]);
+    const uint2 c = *reinterpret_cast<const uint2*>(qx + r * cols + k0);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = e4m3_to_f(((i < 4 ? c.x : c.y) >> (8 * (i & 3))) & 0xffu) * s;
+    store8<OUT>(out, r * cols + k0, v);
+}
+
+// NVFP4 dequantize (reference eager quantization.py:178-219): every step is rounded to
+// the output dtype: total = round(round(g) * s8); out = round(E2M1(c) * total).
+template <int OUT>
+__global__ __launch_bounds__(kThreads) void dequantize_nvfp4_kernel(const uint8_t* __restrict__ qx,
+                                                                    const float* __restrict__ gptr,
+                                                                    const uint8_t* __restrict__ sc,
+                                                                    void* __restrict__ out, int64_t rows,
+                                                                    int64_t cols, int64_t n_cb, bool hi_first) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t per_row = cols / 8;
+    if (t >= rows * per_row) return;
+    const int64_t r = t / per_row;
+    const int64_t k0 = (t - r * per_row) * 8;
+    const float total = round_to<OUT>(round_to<OUT>(gptr[0]) * e4m3_to_f(sc[swz_offset(r, k0 / 16, n_cb)]));
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(qx + r * (cols / 2) + k0 / 2);
+    float v[8];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t b = (w >> (8 * p)) & 0xffu;
+        uint32_t c0 = hi_first ? (b >> 4) : (b & 15u);
+        uint32_t c1 = hi_first ? (b & 15u) : (b >> 4);
+        v[2 * p] = round_to<OUT>(e2m1_to_f(c0) * total);
+        v[2 * p + 1] = round_to<OUT>(e2m1_to_f(c1) * total);
+    }
+    store8<OUT>(out, r * cols + k0, v);
+}
+
+}  // namespace ckh
+
+using namespace ckh;
+
+extern "C" int ckh_quantize_mxfp8(const void* x, void* qx, void* scales, int64_t rows, int64_t cols,
+                                  int64_t orig_rows, int64_t orig_cols, int in_code, uintptr_t stream) {
+    CKH_REQUIRE(x && qx && scales, "quantize_mxfp8: null pointer");
+    CKH_REQUIRE(rows >= orig_rows && cols >= orig_cols && orig_rows >= 0 && orig_cols >= 0,
+                "quantize_mxfp8: padded shape [%lld, %lld] smaller than input [%lld, %lld]", (long long)rows,
+                (long long)cols, (long long)orig_rows, (long long)orig_cols);
+    CKH_REQUIRE(cols % 32 == 0, "quantize_mxfp8: cols (%lld) must be a multiple of 32", (long long)cols);
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "quantize_mxfp8: unsupported input dtype code %d", in_code);
+    CKH_REQUIRE(aligned(qx, 8) && aligned(scales, 4), "quantize_mxfp8: output pointers misaligned");
+    if (rows == 0 || cols == 0) return CKH_OK;
+    const int64_t n_cb = cdiv(cols / 32, 4);
+    const int64_t n_units = rup(rows, 128) * n_cb;
+    const bool vec_ok = aligned(x, 16) && orig_cols % 8 == 0;
+    dim3 grid(static_cast<unsigned>(cdiv(n_units * 16, kThreads)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint8_t* q = static_cast<uint8_t*>(qx);
+    uint32_t* s = static_cast<uint32_t*>(scales);
+#define LAUNCH(I)                                                                                                   \
+    hipLaunchKernelGGL((quantize_mxfp8_kernel<I>), grid, dim3(kThreads), 0, st, x, q, s, rows, cols, orig_rows, \
+                       orig_cols, n_cb, n_units, vec_ok)
+    if (in_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+    return check_launch("quantize_mxfp8");
+}
+
+extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void* qx, void* scales, int64_t rows,
+                                  int64_t cols, int64_t orig_rows, int64_t orig_cols, float epsilon, int in_code,
+                                  int hi_first, uintptr_t stream) {
+    (void)epsilon;  // accepted for ABI compatibility; the reference ignores it too
+    CKH_REQUIRE(x && global_scale && qx && scales, "quantize_nvfp4: null pointer");
+    CKH_REQUIRE(rows >= orig_rows && cols >= orig_cols && orig_rows >= 0 && orig_cols >= 0,
+                "quantize_nvfp4: padded shape smaller than input");
+    CKH_REQUIRE(cols % 16 == 0, "quantize_nvfp4: cols (%lld) must be a multiple of 16", (long long)cols);
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "quantize_nvfp4: unsupported input dtype code %d", in_code);
+    CKH_REQUIRE(aligned(qx, 4) && aligned(scales, 4), "quantize_nvfp4: output pointers misaligned");
+    if (rows == 0 || cols == 0) return CKH_OK;
+    const int64_t n_cb = cdiv(cols / 16, 4);
+    const int64_t n_units = rup(rows, 128) * n_cb;
+    const bool vec_ok = aligned(x, 16) && orig_cols % 8 == 0;
+    dim3 grid(static_cast<unsigned>(cdiv(n_units * 8, kThreads)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float* g = static_cast<const float*>(global_scale);
+    uint8_t* q = static_cast<uint8_t*>(qx);
+    uint32_t* s = static_cast<uint32_t*>(scales);
+    const bool hf = hi_first != 0;
+#define LAUNCH(I)                                                                                              \
+    hipLaunchKernelGGL((quantize_nvfp4_kernel<I>), grid, dim3(kThreads), 0, st, x, g, q, s, rows, cols, \
+                       orig_rows, orig_cols, n_cb, n_units, vec_ok, hf)
+    if (in_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+    return check_launch("quantize_nvfp4");
+}
+
+extern "C" int ckh_dequantize_mxfp8(const void* qx, const void* scales, void* out, int64_t rows, int64_t cols,
+                                    int out_code, uintptr_t stream) {
+    CKH_REQUIRE(qx && scales && out, "dequantize_mxfp8: null pointer");
+    CKH_REQUIRE(rows >= 0 && cols % 32 == 0, "dequantize_mxfp8: cols (%lld) must be a multiple of 32",
+                (long long)cols);
+    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
+                "dequantize_mxfp8: unsupported output dtype code %d", out_code);
+    CKH_REQUIRE(aligned(qx, 8) && aligned(out, 16), "dequantize_mxfp8: pointers misaligned");
+    if (rows == 0 || cols == 0) return CKH_OK;
+    const int64_t n_cb = cdiv(cols / 32, 4);
+    dim3 grid(static_cast<unsigned>(cdiv(rows * (cols / 8), kThreads)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const uint8_t* q = static_cast<const uint8_t*>(qx);
+    const uint8_t* s = static_cast<const uint8_t*>(scales);
+#define LAUNCH(O) hipLaunchKernelGGL((dequantize_mxfp8_kernel<O>), grid, dim3(kThreads), 0, st, q, s, out, rows, cols, n_cb)
+    if (out_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (out_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+    return check_launch("dequantize_mxfp8");
+}
+
+extern "C" int ckh_dequantize_nvfp4(const void* qx, const void* global_scale, const void* scales, void* out,
+                                    int64_t rows, int64_t cols, int out_code, int hi_first, uintptr_t stream) {
+    CKH_REQUIRE(qx && global_scale && scales && out, "dequantize_nvfp4: null pointer");
+    CKH_REQUIRE(rows >= 0 && cols % 16 == 0, "dequantize_nvfp4: cols (%lld) must be a multiple of 16",
+                (long long)cols);
+    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
+                "dequantize_nvfp4: unsupported output dtype code %d", out_code);
+    CKH_REQUIRE(aligned(qx, 4) && aligned(out, 16), "dequantize_nvfp4: pointers misaligned");
+    if (rows == 0 || cols == 0) return CKH_OK;
+    const int64_t n_cb = cdiv(cols / 16, 4);
+    dim3 grid(static_cast<unsigned>(cdiv(rows * (cols / 8), kThreads)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const uint8_t* q = static_cast<const uint8_t*>(qx);
+    const float* g = static_cast<const float*>(global_scale);
+    const uint8_t* s = static_cast<const uint8_t*>(scales);
+    const bool hf = hi_first != 0;
+#define LAUNCH(O) \
+    hipLaunchKernelGGL((dequantize_nvfp4_kernel<O>), grid, dim3(kThreads), 0, st, q, g, s, out, rows, cols, n_cb, hf)
+    if (out_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (out_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+    return check_launch("dequantize_nvfp4");
+}

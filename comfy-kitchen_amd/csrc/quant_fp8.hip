@@ -1,0 +1,182 @@
+// Per-tensor FP8 quantize / dequantize: HBM-streaming kernels for gfx950.
+//
+// Arithmetic is the reference eager backend's, step for step, so codes are bit-exact:
+//   quantize   (backends/eager/quantization.py:53-55):
+//       r = (1/scale) rounded to x's dtype; t = x*r rounded to x's dtype;
+//       t = clamp(t, +-max); code = round-to-nearest-even FP8(t)
+//   dequantize (quantization.py:60): out = x.to(out) * scale.to(out), rounded to out.
+// For bf16/f16 inputs the product of two 16-bit floats is exact in fp32, so rounding
+// the fp32 product to the 16-bit type equals the 16-bit multiply of the reference.
+//
+// Launch shape: 256 threads, 16 elements per thread (one 16-byte FP8 store; two
+// 16-byte loads for 16-bit inputs), one tile per thread, no grid-stride loop: the
+// configs have >= 3k workgroups, enough to fill 256 CUs several times over.
+#include "ckh_common.h"
+
+namespace ckh {
+
+constexpr int kThreads = 256;
+constexpr int kPerThread = 16;
+
+template <int OUT>
+__device__ __forceinline__ uint32_t encode_fp8(float t) {
+    if constexpr (OUT == CKH_E4M3) {
+        t = t > 448.0f ? 448.0f : (t < -448.0f ? -448.0f : t);  // NaN passes through
+        return f_to_e4m3(t);
+    } else {
+        t = t > 57344.0f ? 57344.0f : (t < -57344.0f ? -57344.0f : t);
+        return f_to_e5m2(t);
+    }
+}
+
+template <int IN, int OUT, bool VEC>
+__global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __restrict__ x,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ out, int64_t n) {
+    const float r = round_to<IN>(1.0f / scale[0]);
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kPerThread;
+    constexpr int ES = ElemSize<IN>::value;
+    if (VEC && i0 + kPerThread <= n) {
+        float v[16];
+        load8<IN>(static_cast<const char*>(x) + i0 * ES, *reinterpret_cast<float(*)[8]>(&v[0]));
+        load8<IN>(static_cast<const char*>(x) + (i0 + 8) * ES, *reinterpret_cast<float(*)[8]>(&v[8]));
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
+            w[q] = acc;
+        }
+        *reinterpret_cast<uint4*>(out + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i)
+            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+    }
+}
+
+template <int IN>
+__device__ __forceinline__ float decode_fp8(uint32_t c) {
+    return IN == CKH_E4M3 ? e4m3_to_f(c) : e5m2_to_f(c);
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
+    if constexpr (OUT == CKH_F32) reinterpret_cast<float*>(out)[i] = v;
+    else if constexpr (OUT == CKH_BF16) reinterpret_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(f_to_bf16(v));
+    else reinterpret_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(f_to_f16(v));
+}
+
+// Store 16 rounded outputs starting at element i (16-byte aligned).
+template <int OUT>
+__device__ __forceinline__ void store16(void* out, int64_t i, const float (&v)[16]) {
+    if constexpr (OUT == CKH_F32) {
+        float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+        uint32_t w[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16(v[2 * q]) : f_to_f16(v[2 * q]);
+            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
+            w[q] = lo | (hi << 16);
+        }
+        uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i);
+        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+template <int IN, int OUT, bool VEC>
+__global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t* __restrict__ x,
+                                                                  const float* __restrict__ scale,
+                                                                  void* __restrict__ out, int64_t n) {
+    const float s = round_to<OUT>(scale[0]);
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kPerThread;
+    if (VEC && i0 + kPerThread <= n) {
+        uint4 c = *reinterpret_cast<const uint4*>(x + i0);
+        uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = decode_fp8<IN>((cw[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
+        store16<OUT>(out, i0, v);
+    } else {
+        for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
+    }
+}
+
+}  // namespace ckh
+
+using namespace ckh;
+
+#define CKH_DISPATCH_VEC(vec, ...) \
+    do {                            \
+        if (vec) {                  \
+            constexpr bool V = true; \
+            __VA_ARGS__;            \
+        } else {                    \
+            constexpr bool V = false; \
+            __VA_ARGS__;            \
+        }                           \
+    } while (0)
+
+extern "C" int ckh_quantize_fp8(const void* x, const void* scale, void* out, int64_t numel, int in_code,
+                                int out_code, uintptr_t stream) {
+    CKH_REQUIRE(numel >= 0, "quantize_fp8: numel < 0");
+    if (numel == 0) return CKH_OK;
+    CKH_REQUIRE(x && scale && out, "quantize_fp8: null pointer");
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "quantize_fp8: unsupported input dtype code %d", in_code);
+    CKH_REQUIRE(out_code == CKH_E4M3 || out_code == CKH_E5M2, "quantize_fp8: unsupported output dtype code %d",
+                out_code);
+    const bool vec = aligned(x, 16) && aligned(out, 16);
+    dim3 grid(static_cast<unsigned>(cdiv(numel, kThreads * kPerThread)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float* sp = static_cast<const float*>(scale);
+    uint8_t* o = static_cast<uint8_t*>(out);
+#define LAUNCH_Q(I, O)                                                                              \
+    CKH_DISPATCH_VEC(vec, hipLaunchKernelGGL((quantize_fp8_kernel<I, O, V>), grid, dim3(kThreads), 0, st, \
+                                             x, sp, o, numel))
+    if (out_code == CKH_E4M3) {
+        if (in_code == CKH_F32) LAUNCH_Q(CKH_F32, CKH_E4M3);
+        else if (in_code == CKH_F16) LAUNCH_Q(CKH_F16, CKH_E4M3);
+        else LAUNCH_Q(CKH_BF16, CKH_E4M3);
+    } else {
+        if (in_code == CKH_F32) LAUNCH_Q(CKH_F32, CKH_E5M2);
+        else if (in_code == CKH_F16) LAUNCH_Q(CKH_F16, CKH_E5M2);
+        else LAUNCH_Q(CKH_BF16, CKH_E5M2);
+    }
+#undef LAUNCH_Q
+    return check_launch("quantize_fp8");
+}
+
+extern "C" int ckh_dequantize_fp8(const void* x, const void* scale, void* out, int64_t numel, int in_code,
+                                  int out_code, uintptr_t stream) {
+    CKH_REQUIRE(numel >= 0, "dequantize_fp8: numel < 0");
+    if (numel == 0) return CKH_OK;
+    CKH_REQUIRE(x && scale && out, "dequantize_fp8: null pointer");
+    CKH_REQUIRE(in_code == CKH_E4M3 || in_code == CKH_E5M2, "dequantize_fp8: unsupported input dtype code %d",
+                in_code);
+    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
+                "dequantize_fp8: unsupported output dtype code %d", out_code);
+    const bool vec = aligned(x, 16) && aligned(out, 16);
+    dim3 grid(static_cast<unsigned>(cdiv(numel, kThreads * kPerThread)));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float* sp = static_cast<const float*>(scale);
+    const uint8_t* xi = static_cast<const uint8_t*>(x);
+#define LAUNCH_DQ(I, O)                                                                               \
+    CKH_DISPATCH_VEC(vec, hipLaunchKernelGGL((dequantize_fp8_kernel<I, O, V>), grid, dim3(kThreads), 0, st, \
+                                             xi, sp, out, numel))
+    if (in_code == CKH_E4M3) {
+        if (out_code == CKH_F32) LAUNCH_DQ(CKH_E4M3, CKH_F32);
+        else if (out_code == CKH_F16) LAUNCH_DQ(CKH_E4M3, CKH_F16);
+        else LAUNCH_DQ(CKH_E4M3, CKH_BF16);
+    } else {
+        if (out_code == CKH_F32) LAUNCH_DQ(CKH_E5M2, CKH_F32);
+        else if (out_code == CKH_F16) LAUNCH_DQ(CKH_E5M2, CKH_F16);
+        else LAUNCH_DQ(CKH_E5M2, CKH_BF16);
+    }
+#undef LAUNCH_DQ
+    return check_launch("dequantize_fp8");
+}

@@ -1,0 +1,82 @@
+"""Loader for tests/golden/known_answers.json (hand-derived known-answer vectors)."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import torch
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "known_answers.json"
+NAN = "nan"
+
+
+def _load() -> dict:
+    return json.loads(GOLDEN.read_text())
+
+
+def _code(s):
+    return NAN if s == NAN else int(s, 16)
+
+
+def _expand(spec: dict, n: int, conv) -> list:
+    out = [conv(spec["fill"])] * n
+    for k, v in spec.get("set", {}).items():
+        out[int(k)] = conv(v)
+    return out
+
+
+def fp8_quant_cases():
+    """(x bf16 [1], scale f32 [1], output dtype, expected code)"""
+    res = []
+    for c in _load()["quantize_per_tensor_fp8"]:
+        dt = torch.float8_e4m3fn if c["out"] == "e4m3" else torch.float8_e5m2
+        res.append((torch.tensor([c["x"]], dtype=torch.bfloat16), torch.tensor([c["scale"]], dtype=torch.float32),
+                    dt, int(c["code"], 16)))
+    return res
+
+
+def fp8_dequant_cases():
+    """(codes uint8 [1] viewed as e4m3, scale f32 [1], expected bf16 bits)"""
+    res = []
+    for c in _load()["dequantize_per_tensor_fp8"]:
+        q = torch.tensor([int(c["code"], 16)], dtype=torch.uint8).view(torch.float8_e4m3fn)
+        res.append((q, torch.tensor([c["scale"]], dtype=torch.float32), int(c["bf16"], 16)))
+    return res
+
+
+def mxfp8_cases():
+    """(block bf16 [32], expected scale byte, expected codes list[int | 'nan'])"""
+    res = []
+    for c in _load()["quantize_mxfp8"]:
+        x = torch.tensor(_expand(c["block"], 32, float), dtype=torch.bfloat16)
+        res.append((x, int(c["scale"], 16), _expand(c["codes"], 32, _code)))
+    return res
+
+
+def nvfp4_cases():
+    """(block bf16 [16], g f32 [1], expected scale byte, expected unpacked codes)"""
+    res = []
+    for c in _load()["quantize_nvfp4"]:
+        x = torch.tensor(c["block"], dtype=torch.bfloat16)
+        res.append((x, torch.tensor([c["g"]], dtype=torch.float32), int(c["scale"], 16), list(c["codes"]),
+                    [int(b, 16) for b in c.get("packed_hi_first", [])]))
+    return res
+
+
+def codes_match(got: list[int], want: list) -> bool:
+    """Byte-wise compare where 'nan' accepts either FP8 NaN code."""
+    for g, w in zip(got, want):
+        if w == NAN:
+            if g & 0x7F != 0x7F:
+                return False
+        elif g != w:
+            return False
+    return len(got) == len(want)
+
+
+def unpack(packed: torch.Tensor, hi_first: bool = True) -> list[int]:
+    out = []
+    for b in packed.reshape(-1).tolist():
+        hi, lo = b >> 4, b & 15
+        out += [hi, lo] if hi_first else [lo, hi]
+    return out

@@ -1,0 +1,218 @@
+"""HIP quantizers / dequantizers vs the CPU oracle: bit-exact codes, scales and outputs.
+
+Bar: every code byte, every scale byte (including swizzle padding) and every
+dequantized element equal to the oracle's (the reference eager arithmetic).  NaN
+results compare as NaN-equivalent (any NaN code), since the reference's own CPU paths
+emit either NaN encoding.
+"""
+import pytest
+import torch
+
+import comfy_kitchen as ck
+import kat
+from conftest import bits
+from oracle import eager_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _fp8_equal(got: torch.Tensor, want: torch.Tensor, dt=torch.float8_e4m3fn):
+    g, w = bits(got).reshape(-1), bits(want).reshape(-1)
+    if dt == torch.float8_e4m3fn:
+        gn, wn = (g & 0x7F) == 0x7F, (w & 0x7F) == 0x7F
+    else:
+        gn, wn = (g & 0x7F) > 0x7C, (w & 0x7F) > 0x7C
+    assert torch.equal(gn, wn), f"NaN positions differ: {int((gn != wn).sum())}"
+    bad = (g != w) & ~wn
+    assert int(bad.sum()) == 0, f"{int(bad.sum())} of {g.numel()} codes differ; first at {bad.nonzero()[:5].flatten().tolist()}"
+
+
+# ------------------------------------------------------------- known answers
+@pytest.mark.parametrize("case", range(len(kat.fp8_quant_cases())))
+def test_kat_quantize_fp8(case, hip, dev):
+    x, scale, dt, want = kat.fp8_quant_cases()[case]
+    got = ck.quantize_per_tensor_fp8(x.to(dev), scale.to(dev), dt)
+    assert bits(got).item() == want
+
+
+@pytest.mark.parametrize("case", range(len(kat.fp8_dequant_cases())))
+def test_kat_dequantize_fp8(case, hip, dev):
+    q, scale, want = kat.fp8_dequant_cases()[case]
+    got = ck.dequantize_per_tensor_fp8(q.to(dev), scale.to(dev), torch.bfloat16)
+    assert bits(got).item() & 0xFFFF == want
+
+
+def test_kat_mxfp8(hip, dev):
+    cases = kat.mxfp8_cases()
+    x = torch.stack([c[0] for c in cases])  # one block per row
+    q, s = ck.quantize_mxfp8(x.to(dev))
+    e = ref.from_blocked(bits(s), len(cases), 1)
+    for r, (_, want_s, want_c) in enumerate(cases):
+        assert e[r, 0].item() == want_s, r
+        assert kat.codes_match(bits(q[r]).tolist(), want_c), (r, bits(q[r]).tolist())
+
+
+def test_kat_nvfp4(hip, dev):
+    for x, g, want_s, want_c, want_p in kat.nvfp4_cases():
+        q, s = ck.quantize_nvfp4(x.reshape(1, 16).to(dev), g.to(dev))
+        assert ref.from_blocked(bits(s), 1, 1).item() == want_s
+        assert kat.unpack(q.cpu()) == want_c
+        if want_p:
+            assert bits(q).tolist() == [want_p]
+
+
+# ------------------------------------------------------- per-tensor FP8
+@pytest.mark.parametrize("out_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("scale", [1.0, 0.9481481481481482, 10.0 / 448, 2.0 ** -20, 3.0e4, 0.7])
+def test_quantize_fp8_every_bf16(scale, out_dtype, hip, dev):
+    """All 65,536 bf16 bit patterns (including NaN, inf, subnormals) at several scales."""
+    x = ref.all_bf16()
+    s = torch.tensor([scale])
+    want = ref.quantize_per_tensor_fp8(x.clone(), s, out_dtype)
+    got = ck.quantize_per_tensor_fp8(x.to(dev), s.to(dev), out_dtype)
+    _fp8_equal(got, want, out_dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1000, 1000), (1024, 2048), (7, 13), (1,), (0, 5)])
+def test_quantize_fp8_random(dtype, shape, hip, dev, seed):
+    x = (torch.randn(shape) * 30).to(dtype)
+    scale = torch.tensor([0.173])
+    want = ref.quantize_per_tensor_fp8(x.clone(), scale)
+    got = ck.quantize_per_tensor_fp8(x.to(dev), scale.to(dev))
+    assert got.shape == x.shape and got.dtype == torch.float8_e4m3fn
+    _fp8_equal(got, want)
+
+
+def test_quantize_fp8_misaligned_view(hip, dev, seed):
+    """A 2-byte-offset view takes the scalar path and still matches."""
+    x = (torch.randn(4097) * 5).bfloat16()
+    want = ref.quantize_per_tensor_fp8(x[1:].clone(), torch.tensor([0.05]))
+    xd = x.to(dev)[1:]
+    got = ck.quantize_per_tensor_fp8(xd, torch.tensor([0.05], device=dev))
+    _fp8_equal(got, want)
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("scale", [1.0, 1.0048828125, 0.00123, 371.5])
+def test_dequantize_fp8_every_code(in_dtype, out_dtype, scale, hip, dev):
+    q = torch.arange(256, dtype=torch.int32).to(torch.uint8).repeat(40).view(in_dtype)
+    s = torch.tensor([scale])
+    want = ref.dequantize_per_tensor_fp8(q, s, out_dtype)
+    got = ck.dequantize_per_tensor_fp8(q.to(dev), s.to(dev), out_dtype)
+    assert got.dtype == out_dtype
+    w, g = want.float(), got.cpu().float()
+    nan = torch.isnan(w)
+    assert torch.equal(nan, torch.isnan(g))
+    assert torch.equal(bits(got)[~nan], bits(want)[~nan])
+
+
+def test_c1_full_size_round_trip(hip, dev):
+    """Config 1 at full size: codes bit-exact vs the oracle, dequantize bit-exact."""
+    import bench
+
+    x, scale = bench.make_c1()
+    want_q = ref.quantize_per_tensor_fp8(x.clone(), scale)
+    want_dq = ref.dequantize_per_tensor_fp8(want_q, scale)
+    q = ck.quantize_per_tensor_fp8(x.to(dev), scale.to(dev))
+    _fp8_equal(q, want_q)
+    dq = ck.dequantize_per_tensor_fp8(q, scale.to(dev))
+    assert torch.equal(bits(dq), bits(want_dq))
+
+
+# ----------------------------------------------------------------- MXFP8
+def _check_mx(x, pad):
+    want_q, want_s = ref.quantize_mxfp8(x, pad_32x=pad)
+    q, s = ck.quantize_mxfp8(x.cuda(), pad_32x=pad)
+    assert q.shape == want_q.shape and s.shape == want_s.shape
+    assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float8_e8m0fnu
+    assert torch.equal(bits(s), bits(want_s)), "scale bytes differ"
+    _fp8_equal(q, want_q)
+    return q, s
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (96, 32), (130, 4128)])
+def test_quantize_mxfp8(dtype, m, k, hip, seed):
+    x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1) * 2)).to(dtype)
+    x[0, :32] = 0  # zero block
+    x[1, :31] = 0
+    x[1, 31] = -3.0
+    _check_mx(x, pad=False)
+
+
+@pytest.mark.parametrize("m,k", [(65, 96), (33, 64), (100, 100), (1, 1), (129, 31)])
+def test_quantize_mxfp8_padded(m, k, hip, seed):
+    x = (torch.randn(m, k) * 10).bfloat16()
+    _check_mx(x, pad=True)
+
+
+def test_quantize_mxfp8_config3_full(hip):
+    import bench
+
+    _check_mx(bench.make_c3(), pad=False)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_mxfp8(out_dtype, hip, seed):
+    x = (torch.randn(256, 512) * torch.exp(torch.randn(256, 1) * 4)).bfloat16()
+    q, s = ref.quantize_mxfp8(x)
+    want = ref.dequantize_mxfp8(q, s, out_dtype)
+    got = ck.dequantize_mxfp8(q.cuda(), s.cuda(), out_dtype)
+    assert torch.equal(bits(got), bits(want))
+
+
+# ----------------------------------------------------------------- NVFP4
+def _check_nv(x, g, pad, hi_first=True):
+    want_q, want_s = ref.quantize_nvfp4(x, g, pad_16x=pad, hi_first=hi_first)
+    q, s = ck.quantize_nvfp4(x.cuda(), g.cuda(), pad_16x=pad, hi_first=hi_first)
+    assert q.shape == want_q.shape and s.shape == want_s.shape
+    assert q.dtype == torch.uint8 and s.dtype == torch.float8_e4m3fn
+    assert torch.equal(bits(s), bits(want_s)), "scale bytes differ"
+    assert torch.equal(q.cpu(), want_q), f"{int((q.cpu() != want_q).sum())} code bytes differ"
+    return q, s
+
+
+@pytest.mark.parametrize("hi_first", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (16, 64)])
+def test_quantize_nvfp4(dtype, m, k, hi_first, hip, seed):
+    x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1))).to(dtype)
+    x[0, :16] = 0
+    g = (x.float().abs().amax() / 2688).reshape(1)
+    _check_nv(x, g, pad=False, hi_first=hi_first)
+
+
+@pytest.mark.parametrize("m,k", [(129, 128), (33, 65), (100, 100), (1, 1)])
+def test_quantize_nvfp4_padded(m, k, hip, seed):
+    x = (torch.randn(m, k) * 4).bfloat16()
+    g = (x.float().abs().amax() / 2688).reshape(1)
+    _check_nv(x, g, pad=True)
+
+
+def test_quantize_nvfp4_config5_activation_full(hip):
+    import bench
+
+    a, _, ga, _ = bench.make_c5()
+    _check_nv(a, ga, pad=False)
+
+
+def test_nvfp4_hi_first_swap_on_gpu(hip, seed):
+    x = (torch.randn(64, 128) * 4).bfloat16().cuda()
+    g = (x.float().abs().amax() / 2688).reshape(1)
+    qh, sh = ck.quantize_nvfp4(x, g, hi_first=True)
+    ql, sl = ck.quantize_nvfp4(x, g, hi_first=False)
+    assert torch.equal(ck.swap_nibbles(qh), ql)
+    assert torch.equal(bits(sh), bits(sl))
+
+
+@pytest.mark.parametrize("hi_first", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_nvfp4(out_dtype, hi_first, hip, seed):
+    x = (torch.randn(256, 512) * torch.exp(torch.randn(256, 1))).bfloat16()
+    g = (x.float().abs().amax() / 2688).reshape(1)
+    q, s = ref.quantize_nvfp4(x, g, hi_first=hi_first)
+    want = ref.dequantize_nvfp4(q, g, s, out_dtype, hi_first=hi_first)
+    got = ck.dequantize_nvfp4(q.cuda(), g.cuda(), s.cuda(), out_dtype, hi_first=hi_first)
+    assert torch.equal(bits(got), bits(want))

@@ -1,0 +1,104 @@
+"""HIP RoPE vs the CPU oracle (reference eager rope.py:7-18).
+
+Bar (north star): within 1 ULP of the output dtype for fp32 freqs.  With 16-bit
+freqs the reference computes in that 16-bit type; the kernel emulates each rounding,
+so the same 1-ULP bound is asserted there too.
+"""
+import pytest
+import torch
+
+import comfy_kitchen as ck
+from oracle import eager_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_diff(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a - b| in units in the last place of the 16-bit format (ordered-integer distance)."""
+    ia = a.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    ib = b.detach().cpu().contiguous().view(torch.int16).to(torch.int32)
+    oa = torch.where(ia < 0, -(ia & 0x7FFF), ia)
+    ob = torch.where(ib < 0, -(ib & 0x7FFF), ib)
+    return (oa - ob).abs()
+
+
+def check(got, want, max_ulp=1):
+    assert got.shape == want.shape and got.dtype == want.dtype
+    d = ulp_diff(got, want)
+    assert int(d.max()) <= max_ulp, f"max ulp {int(d.max())}, {int((d > max_ulp).sum())} elements over"
+    return float((d == 0).float().mean())
+
+
+def test_config2_flux_full(hip):
+    import bench
+
+    q, k, f = bench.make_c2()
+    wq, wk = ref.apply_rope(q, k, f)
+    gq, gk = ck.apply_rope(q.cuda(), k.cuda(), f.cuda())
+    exact = min(check(gq, wq), check(gk, wk))
+    print(f"fraction bit-identical: {exact:.6f}")
+    g1 = ck.apply_rope1(q.cuda(), f.cuda())
+    assert torch.equal(g1.cpu(), gq.cpu())
+
+
+@pytest.mark.parametrize("op", ["apply_rope", "apply_rope1"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("freqs_dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("name,layout,shape", [
+    ("FLUX", "BHND", (1, 24, 4352, 128)),
+    ("LTX", "BHND", (2, 32, 4996, 64)),
+    ("ZIMAGE", "BNHD", (1, 4096, 30, 128)),
+], ids=["FLUX", "LTX", "ZIMAGE"])
+def test_reference_configs(op, dtype, freqs_dtype, name, layout, shape, hip, seed):
+    """The reference's own RoPE test configs (tests/test_rope.py:15-35)."""
+    if layout == "BHND":
+        b, h, n, d = shape
+        fshape = (b, 1, n, d // 2, 2, 2)
+    else:
+        b, n, h, d = shape
+        fshape = (1, n, 1, d // 2, 2, 2)
+    f = torch.randn(fshape).to(freqs_dtype)
+    xq = torch.randn(shape).to(dtype)
+    if op == "apply_rope":
+        xk = torch.randn(shape).to(dtype)
+        wq, wk = ref.apply_rope(xq, xk, f)
+        gq, gk = ck.apply_rope(xq.cuda(), xk.cuda(), f.cuda())
+        check(gq, wq)
+        check(gk, wk)
+    else:
+        check(ck.apply_rope1(xq.cuda(), f.cuda()), ref.apply_rope1(xq, f))
+
+
+def test_freqs_longer_than_sequence_is_truncated(hip, seed):
+    x = torch.randn(2, 4, 100, 64).bfloat16()
+    f = torch.randn(1, 1, 130, 32, 2, 2)
+    check(ck.apply_rope1(x.cuda(), f.cuda()), ref.apply_rope1(x, f))
+
+
+def test_fully_broadcast_and_per_batch_freqs(hip, seed):
+    x = torch.randn(3, 5, 7, 32).half()
+    for fshape in [(1, 1, 1, 16, 2, 2), (3, 1, 7, 16, 2, 2), (3, 5, 7, 16, 2, 2), (1, 5, 1, 16, 2, 2)]:
+        f = torch.randn(fshape)
+        check(ck.apply_rope1(x.cuda(), f.cuda()), ref.apply_rope1(x, f))
+
+
+def test_unvectorized_head_dim_and_noncontiguous(hip, seed):
+    x = torch.randn(1, 3, 9, 6).bfloat16()  # head_dim 6: scalar path
+    f = torch.randn(1, 1, 9, 3, 2, 2)
+    check(ck.apply_rope1(x.cuda(), f.cuda()), ref.apply_rope1(x, f))
+    xt = torch.randn(1, 9, 3, 64).bfloat16().transpose(1, 2)  # non-contiguous input
+    f2 = torch.randn(1, 1, 9, 32, 2, 2)
+    check(ck.apply_rope1(xt.cuda(), f2.cuda()), ref.apply_rope1(xt, f2))
+    f3 = torch.randn(1, 1, 9, 32, 2, 2, 2)[..., 0]  # non-contiguous freqs
+    check(ck.apply_rope1(xt.cuda(), f3.cuda()), ref.apply_rope1(xt, f3))
+
+
+def test_mismatched_q_k_shapes(hip, seed):
+    q = torch.randn(1, 8, 16, 64).bfloat16()
+    k = torch.randn(1, 2, 16, 64).bfloat16()
+    f = torch.randn(1, 1, 16, 32, 2, 2)
+    gq, gk = ck.apply_rope(q.cuda(), k.cuda(), f.cuda())
+    wq, wk = ref.apply_rope(q, k, f)
+    check(gq, wq)
+    check(gk, wk)

@@ -1,0 +1,191 @@
+"""Pin the CPU oracle (oracle/eager_ref.py) before trusting it.
+
+Three independent checks, none of which retypes the oracle's own formula:
+  * hand-derived known answers (tests/golden/known_answers.json);
+  * oracle/scalar_ref.c, a scalar restatement that rounds by brute-force nearest-value
+    search instead of bit manipulation, compared exhaustively over all 65,536 bf16
+    inputs and over large random samples of blocks;
+  * closed-form layout identities (swizzle offsets, round trips, nibble swap).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import kat
+from oracle import eager_ref as ref
+
+pytestmark = []
+
+
+def _u8(t: torch.Tensor) -> list[int]:
+    return t.contiguous().view(torch.uint8).reshape(-1).tolist()
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data_as(ctypes.c_void_p).value
+
+
+# ------------------------------------------------------------- known answers
+@pytest.mark.parametrize("case", range(len(kat.fp8_quant_cases())))
+def test_kat_quantize_fp8_oracle_and_scalar(case, scalar_ref):
+    x, scale, dt, want = kat.fp8_quant_cases()[case]
+    assert _u8(ref.quantize_per_tensor_fp8(x.clone(), scale, dt)) == [want]
+    xb = ref.bf16_bits(x).copy()
+    out = np.zeros(1, dtype=np.uint8)
+    scalar_ref.ref_quantize_fp8_bf16(_ptr(xb), 1, float(scale), int(dt == torch.float8_e5m2), _ptr(out))
+    assert int(out[0]) == want
+
+
+@pytest.mark.parametrize("case", range(len(kat.fp8_dequant_cases())))
+def test_kat_dequantize_fp8_oracle(case):
+    q, scale, want = kat.fp8_dequant_cases()[case]
+    got = ref.dequantize_per_tensor_fp8(q, scale, torch.bfloat16)
+    assert int(got.view(torch.int16).item()) & 0xFFFF == want
+
+
+@pytest.mark.parametrize("case", range(len(kat.mxfp8_cases())))
+def test_kat_mxfp8_oracle_and_scalar(case, scalar_ref):
+    x, want_scale, want_codes = kat.mxfp8_cases()[case]
+    q, s = ref.quantize_mxfp8(x.reshape(1, 32))
+    assert ref.from_blocked(s.view(torch.uint8), 1, 1).item() == want_scale
+    assert kat.codes_match(_u8(q), want_codes), _u8(q)
+    xb = ref.bf16_bits(x).copy()
+    e, c = np.zeros(1, np.uint8), np.zeros(32, np.uint8)
+    scalar_ref.ref_quantize_mxfp8_row_bf16(_ptr(xb), 1, _ptr(e), _ptr(c))
+    assert int(e[0]) == want_scale
+    assert kat.codes_match(c.tolist(), want_codes)
+
+
+@pytest.mark.parametrize("case", range(len(kat.nvfp4_cases())))
+def test_kat_nvfp4_oracle_and_scalar(case, scalar_ref):
+    x, g, want_scale, want_codes, want_packed = kat.nvfp4_cases()[case]
+    q, s = ref.quantize_nvfp4(x.reshape(1, 16), g)
+    assert ref.from_blocked(s.view(torch.uint8), 1, 1).item() == want_scale
+    assert kat.unpack(q) == want_codes
+    if want_packed:
+        assert _u8(q) == want_packed
+    xb = ref.bf16_bits(x).copy()
+    sc, c = np.zeros(1, np.uint8), np.zeros(16, np.uint8)
+    scalar_ref.ref_quantize_nvfp4_row_bf16(_ptr(xb), 1, float(g), _ptr(sc), _ptr(c))
+    assert int(sc[0]) == want_scale and c.tolist() == want_codes
+
+
+# -------------------------------------------------- exhaustive vs scalar C
+@pytest.mark.parametrize("out_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("scale", [1.0, 0.9481481481481482, 10.0 / 448, 2.0 ** -20, 3.0e4, 0.7])
+def test_quantize_fp8_all_bf16_vs_scalar(scale, out_dtype, scalar_ref):
+    x = ref.all_bf16()
+    got = _u8(ref.quantize_per_tensor_fp8(x.clone(), torch.tensor([scale]), out_dtype))
+    xb = ref.bf16_bits(x).copy()
+    want = np.zeros(65536, np.uint8)
+    scalar_ref.ref_quantize_fp8_bf16(_ptr(xb), 65536, scale, int(out_dtype == torch.float8_e5m2), _ptr(want))
+    got = np.array(got, np.uint8)
+    nan_lo = (want & 0x7F) == 0x7F if out_dtype == torch.float8_e4m3fn else (want & 0x7F) > 0x7C
+    nan_got = (got & 0x7F) == 0x7F if out_dtype == torch.float8_e4m3fn else (got & 0x7F) > 0x7C
+    assert np.array_equal(nan_lo, nan_got)
+    mism = np.nonzero((got != want) & ~nan_lo)[0]
+    assert mism.size == 0, f"{mism.size} mismatches, first x bits {xb[mism[:5]]}"
+
+
+def test_fp8_library_cast_vs_bruteforce(scalar_ref):
+    """torch's fp32->E4M3/E5M2 cast (the routine the oracle relies on) is RNE on the clamped range."""
+    x = ref.all_bf16().float()
+    for dt, lim, fn in ((torch.float8_e4m3fn, 448.0, scalar_ref.ref_f32_to_e4m3),
+                        (torch.float8_e5m2, 57344.0, scalar_ref.ref_f32_to_e5m2)):
+        v = x[(x.abs() <= lim)]
+        got = _u8(v.to(dt))
+        want = [fn(float(f)) for f in v.tolist()]
+        assert got == want
+
+
+def test_e2m1_oracle_vs_bruteforce(scalar_ref):
+    g = torch.Generator().manual_seed(0)
+    pieces = [ref.all_bf16().float(),
+              (torch.rand(200_000, generator=g) * 13 - 6.5)]
+    mids = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0, 1.0, 0.5])
+    for m in mids.tolist():
+        for k in range(-4, 5):
+            f = np.float32(m).view(np.int32) + k
+            pieces.append(torch.tensor([np.int32(f).view(np.float32), -np.int32(f).view(np.float32)]))
+    x = torch.cat(pieces)
+    x = x[~torch.isnan(x)].clamp(-6.0, 6.0)
+    got = ref.f32_to_e2m1(x).tolist()
+    want = [scalar_ref.ref_f32_to_e2m1(float(f)) for f in x.tolist()]
+    assert got == want
+
+
+def _lognormal_rows(rows, cols, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 3)
+    x[0, :32] = 0.0  # a zero block
+    x[1, 5] = 1e-38  # tiny values
+    return x.to(dtype)
+
+
+def test_mxfp8_oracle_vs_scalar(scalar_ref):
+    x = _lognormal_rows(96, 1024, 1)
+    q, s = ref.quantize_mxfp8(x)
+    e = ref.from_blocked(s.view(torch.uint8), 96, 32).numpy()
+    qn = q.view(torch.uint8).numpy()
+    for r in range(96):
+        xb = ref.bf16_bits(x[r]).copy()
+        ee, cc = np.zeros(32, np.uint8), np.zeros(1024, np.uint8)
+        scalar_ref.ref_quantize_mxfp8_row_bf16(_ptr(xb), 32, _ptr(ee), _ptr(cc))
+        assert np.array_equal(ee, e[r]), r
+        assert np.array_equal(cc, qn[r]), r
+
+
+@pytest.mark.parametrize("g", [1.0, 0.0123, 3.7e-3, 250.0])
+def test_nvfp4_oracle_vs_scalar(g, scalar_ref):
+    x = _lognormal_rows(64, 512, 2)
+    q, s = ref.quantize_nvfp4(x, torch.tensor([g]))
+    sc = ref.from_blocked(s.view(torch.uint8), 64, 32).numpy()
+    codes = np.array([kat.unpack(q[r]) for r in range(64)], np.uint8)
+    for r in range(64):
+        xb = ref.bf16_bits(x[r]).copy()
+        ss, cc = np.zeros(32, np.uint8), np.zeros(512, np.uint8)
+        scalar_ref.ref_quantize_nvfp4_row_bf16(_ptr(xb), 32, g, _ptr(ss), _ptr(cc))
+        assert np.array_equal(ss, sc[r]), r
+        assert np.array_equal(cc, codes[r]), r
+
+
+# -------------------------------------------------------------- layouts
+def test_swizzle_layout_closed_form():
+    """Oracle to_blocked places (r, c) at the 32_4_4 offset formula; padding is zero."""
+    rows, cols = 300, 11
+    src = torch.arange(rows * cols, dtype=torch.int32).reshape(rows, cols) + 1
+    blk = ref.to_blocked(src).reshape(-1)
+    n_cb = -(-cols // 4)
+    for r in range(rows):
+        for c in range(cols):
+            off = (((r // 128) * n_cb + c // 4) * 32 + r % 32) * 16 + ((r % 128) // 32) * 4 + c % 4
+            assert blk[off].item() == src[r, c].item()
+    assert int((blk == 0).sum()) == blk.numel() - rows * cols
+    assert torch.equal(ref.from_blocked(ref.to_blocked(src), rows, cols), src)
+
+
+def test_package_swizzle_matches_oracle():
+    import comfy_kitchen as ck
+
+    g = torch.Generator().manual_seed(3)
+    for rows, cols in [(1, 1), (128, 4), (129, 5), (4608, 96), (33, 320)]:
+        s = torch.randint(0, 255, (rows, cols), generator=g, dtype=torch.uint8)
+        a = ck.to_blocked(s, flatten=False)
+        b = ref.to_blocked(s)
+        assert torch.equal(a, b)
+        assert torch.equal(ck.from_blocked(a, rows, cols), s)
+        assert torch.equal(ck.to_blocked(s).reshape(a.shape), a)
+
+
+def test_swap_nibbles_and_hi_first():
+    import comfy_kitchen as ck
+
+    x = _lognormal_rows(16, 64, 4)
+    g = torch.tensor([0.01])
+    qh, sh = ref.quantize_nvfp4(x, g, hi_first=True)
+    ql, sl = ref.quantize_nvfp4(x, g, hi_first=False)
+    assert torch.equal(ck.swap_nibbles(qh), ql)
+    assert torch.equal(sh.view(torch.uint8), sl.view(torch.uint8))
+    assert torch.equal(ref.dequantize_nvfp4(qh, g, sh), ref.dequantize_nvfp4(ql, g, sl, hi_first=False))
