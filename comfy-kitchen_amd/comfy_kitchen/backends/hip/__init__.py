@@ -356,17 +356,17 @@ def _build_constraints() -> dict:
                                block_scales=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn})),
                                output_type=ParamConstraint(dtypes=floats)),
         "scaled_mm_mxfp8": fc(a=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
-                                                shape_rules=two_d + (DivisibleBy(1, 128),)),
+                                                shape_rules=two_d + (DivisibleBy(1, 32),)),
                               b=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
-                                                shape_rules=two_d + (DivisibleBy(1, 128),)),
+                                                shape_rules=two_d + (DivisibleBy(1, 32),)),
                               block_scale_a=ParamConstraint(dtypes=frozenset({torch.float8_e8m0fnu})),
                               block_scale_b=ParamConstraint(dtypes=frozenset({torch.float8_e8m0fnu})),
                               bias=ParamConstraint(dtypes=floats),
                               out_dtype=ParamConstraint(dtypes=floats)),
         "scaled_mm_nvfp4": fc(a=ParamConstraint(dtypes=frozenset({torch.uint8}),
-                                                shape_rules=two_d + (DivisibleBy(1, 32),)),
+                                                shape_rules=two_d + (DivisibleBy(1, 16),)),
                               b=ParamConstraint(dtypes=frozenset({torch.uint8}),
-                                                shape_rules=two_d + (DivisibleBy(1, 32),)),
+                                                shape_rules=two_d + (DivisibleBy(1, 16),)),
                               tensor_scale_a=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
                               tensor_scale_b=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
                               block_scale_a=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn})),

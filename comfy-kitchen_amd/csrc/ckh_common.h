@@ -47,6 +47,15 @@ __device__ __forceinline__ uint32_t f_to_bf16(float f) {
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
 
+// Hide a value from instruction selection.  Without it the backend folds
+// "fp32 multiply (or FMA), then narrow to f16" into one v_fma_mix*_f16 with a +0
+// addend: that rounds once instead of twice and turns a -0 product into +0, both of
+// which break bit-exactness with the reference's fp32-then-f16 arithmetic.
+__device__ __forceinline__ float opaque(float f) {
+    __asm__("" : "+v"(f));
+    return f;
+}
+
 // binary16 <-> float through the IEEE conversion instructions (round-to-nearest-even,
 // subnormals kept, which is the default FP mode of HIP kernels).
 __device__ __forceinline__ float f16_to_f(uint32_t h) {
@@ -56,7 +65,7 @@ __device__ __forceinline__ float f16_to_f(uint32_t h) {
     return static_cast<float>(v);
 }
 __device__ __forceinline__ uint32_t f_to_f16(float f) {
-    _Float16 v = static_cast<_Float16>(f);
+    _Float16 v = static_cast<_Float16>(opaque(f));
     uint16_t hb;
     __builtin_memcpy(&hb, &v, 2);
     return hb;

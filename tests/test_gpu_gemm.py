@@ -1,0 +1,164 @@
+"""HIP block-scaled GEMMs vs an fp32 matmul of the dequantized operands.
+
+rel-L2 <= 1e-2 against fp32 matmul of the dequantized operands.  The
+kernels multiply the quantized values exactly and accumulate in fp32 MFMAs, so they
+are held far tighter: 1e-4 with an fp32 output (the MFMA's internal reduction is not
+a sequentially rounded fp32 sum; measured ~1.5e-5), and the output rounding with
+bf16/f16 outputs (2^-8 relative per element, well under 1e-2 in L2).
+"""
+import pytest
+import torch
+
+import comfy_kitchen as ck
+from oracle import eager_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+# fp32 output: the MFMA reduction is not an fp32-rounded sequential sum (measured ~1.5e-5)
+REL_L2 = {torch.float32: 1e-4, torch.float16: 1e-3, torch.bfloat16: 4e-3}
+
+
+def rel_l2(got: torch.Tensor, want: torch.Tensor) -> float:
+    got, want = got.float().cpu(), want.float().cpu()
+    return ((got - want).norm() / want.norm().clamp_min(1e-30)).item()
+
+
+def mx_operands(m, n, k, seed, wscale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(m, k, generator=g) * torch.exp(torch.randn(m, 1, generator=g))).bfloat16()
+    w = (torch.randn(n, k, generator=g) * wscale).bfloat16()
+    qx, sx = ref.quantize_mxfp8(x, pad_32x=(k % 32 != 0))
+    qw, sw = ref.quantize_mxfp8(w, pad_32x=(k % 32 != 0))
+    return qx, sx, qw, sw
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (128, 512, 1024), (512, 256, 3072), (100, 300, 256),
+                                   (33, 17, 96), (260, 520, 160), (1, 64, 32), (257, 255, 224)])
+def test_scaled_mm_mxfp8_vs_oracle(m, n, k, out_dtype, hip):
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=m * 7 + n + k)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_scaled_mm_mxfp8_bias(bias_dtype, hip):
+    qx, sx, qw, sw = mx_operands(192, 384, 512, seed=5)
+    bias = (torch.randn(384) * 2).to(bias_dtype)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), bias=bias.cuda(), out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+
+
+def test_scaled_mm_mxfp8_extreme_scales(hip):
+    """Rows spanning ~2^±40 of magnitude: the E8M0 scales, not the codes, carry the range."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(128, 512, generator=g) * torch.exp2(torch.randint(-40, 40, (128, 1), generator=g).float())
+    w = torch.randn(256, 512, generator=g) * torch.exp2(torch.randint(-20, 20, (256, 16), generator=g).float()
+                                                        ).repeat_interleave(32, dim=1)
+    qx, sx = ref.quantize_mxfp8(x.bfloat16())
+    qw, sw = ref.quantize_mxfp8(w.bfloat16())
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.float32)
+    # compare row-normalised: each output row has its own magnitude
+    d = (got.cpu() - want) / want.abs().amax(dim=1, keepdim=True).clamp_min(1e-30)
+    assert d.abs().max().item() <= 5e-4
+
+
+def test_scaled_mm_mxfp8_config4_full(hip):
+    """Config 4 at full size against a GPU fp32 matmul of the (bit-exact) dequantized operands."""
+    import bench
+
+    x = bench.make_c3("cuda")
+    w = bench.make_c4_weight("cuda")
+    qx, sx = ck.quantize_mxfp8(x)
+    qw, sw = ck.quantize_mxfp8(w)
+    got = ck.scaled_mm_mxfp8(qx, qw, sx, sw)
+    dx = ck.dequantize_mxfp8(qx, sx, torch.float32)
+    dw = ck.dequantize_mxfp8(qw, sw, torch.float32)
+    want = torch.matmul(dx, dw.t().contiguous())
+    assert got.shape == (4608, 12288) and got.dtype == torch.bfloat16
+    r = ((got.float() - want).norm() / want.norm()).item()
+    print(f"config 4 rel-L2 vs fp32 matmul of dequantized operands: {r:.3e}")
+    assert r <= 4e-3
+    # and a slice against the CPU oracle end to end
+    rows = slice(0, 256)
+    want_cpu = ref.scaled_mm_mxfp8_ref(qx[rows].cpu(), qw.cpu(), ref.to_blocked(
+        ref.from_blocked(sx.cpu().view(torch.uint8), 4608, 96)[rows]).view(torch.float8_e8m0fnu), sw.cpu(),
+        out_dtype=torch.float32)
+    assert rel_l2(got[rows], want_cpu) <= 4e-3
+
+
+def test_scaled_mm_mxfp8_rejects_bad_shapes(hip):
+    a = torch.zeros(64, 96, dtype=torch.float8_e4m3fn, device="cuda")
+    b = torch.zeros(64, 64, dtype=torch.float8_e4m3fn, device="cuda")
+    s = torch.zeros(128, 4, dtype=torch.float8_e8m0fnu, device="cuda")
+    with pytest.raises((ValueError, RuntimeError)):
+        ck.scaled_mm_mxfp8(a, b, s, s)
+
+
+# --------------------------------------------------------------------- NVFP4
+def nv_operands(m, n, k, seed, wscale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * wscale).bfloat16()
+    gx = (x.float().abs().amax() / 2688).reshape(1)
+    gw = (w.float().abs().amax() / 2688).reshape(1)
+    qx, sx = ref.quantize_nvfp4(x, gx)
+    qw, sw = ref.quantize_nvfp4(w, gw)
+    return qx, sx, gx, qw, sw, gw
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (128, 512, 1024), (512, 256, 5120), (100, 300, 256),
+                                   (33, 17, 96), (260, 520, 160), (16, 64, 32), (257, 255, 224)])
+def test_scaled_mm_nvfp4_vs_oracle(m, n, k, out_dtype, hip):
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=m + 3 * n + k)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32])
+def test_scaled_mm_nvfp4_bias_and_alpha(bias_dtype, hip):
+    qx, sx, gx, qw, sw, gw = nv_operands(192, 384, 512, seed=9)
+    bias = (torch.randn(384) * 0.1).to(bias_dtype)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), bias=bias.cuda(),
+                             out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+    # explicit alpha overrides tensor_scale_a * tensor_scale_b
+    alpha = (gx * gw * 2).cuda()
+    got2 = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.float32,
+                              alpha=alpha)
+    want2 = ref.scaled_mm_nvfp4_ref(qx, qw, gx * 2, gw, sx, sw, out_dtype=torch.float32)
+    assert rel_l2(got2, want2) <= REL_L2[torch.float32]
+
+
+def test_scaled_mm_nvfp4_hi_first_invariance(hip):
+    """Packing order does not change the product when both operands share it."""
+    qx, sx, gx, qw, sw, gw = nv_operands(128, 256, 512, seed=2)
+    a = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.float32)
+    b = ck.scaled_mm_nvfp4(ck.swap_nibbles(qx).cuda(), ck.swap_nibbles(qw).cuda(), gx.cuda(), gw.cuda(), sx.cuda(),
+                           sw.cuda(), out_dtype=torch.float32)
+    assert torch.equal(a, b)
+
+
+def test_scaled_mm_nvfp4_config5_full(hip):
+    """Config 5 at full size against a GPU fp32 matmul of the dequantized operands."""
+    import bench
+
+    a, w, ga, gw = bench.make_c5("cuda")
+    qa, sa = ck.quantize_nvfp4(a, ga)
+    qw, sw = ck.quantize_nvfp4(w, gw)
+    got = ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)
+    da = ck.dequantize_nvfp4(qa, torch.ones_like(ga), sa, torch.float32)  # E2M1 * s8, exact in fp32
+    dw = ck.dequantize_nvfp4(qw, torch.ones_like(gw), sw, torch.float32)
+    want = torch.matmul(da, dw.t().contiguous()) * (ga * gw)
+    assert got.shape == (8192, 13824) and got.dtype == torch.bfloat16
+    r = ((got.float() - want).norm() / want.norm()).item()
+    print(f"config 5 rel-L2 vs fp32 matmul of dequantized operands: {r:.3e}")
+    assert r <= 4e-3
