@@ -47,6 +47,11 @@ __device__ __forceinline__ uint32_t f_to_bf16(float f) {
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
 
+// bfloat16 round-to-nearest-even through the hardware convert (v_cvt_pk_bf16_f32).
+// Checked against f_to_bf16 on all 2^32 inputs on gfx950: identical for every
+// non-NaN input, NaN stays NaN.
+__device__ __forceinline__ uint32_t f_to_bf16_rne(float f);
+
 // Hide a value from instruction selection.  Without it the backend folds
 // "fp32 multiply (or FMA), then narrow to f16" into one v_fma_mix*_f16 with a +0
 // addend: that rounds once instead of twice and turns a -0 product into +0, both of
@@ -71,6 +76,13 @@ __device__ __forceinline__ uint32_t f_to_f16(float f) {
     return hb;
 }
 __device__ __forceinline__ float round_f16(float f) { return f16_to_f(f_to_f16(f)); }
+
+__device__ __forceinline__ uint32_t f_to_bf16_rne(float f) {
+    __bf16 b = static_cast<__bf16>(opaque(f));
+    uint16_t hb;
+    __builtin_memcpy(&hb, &b, 2);
+    return hb;
+}
 
 // Round a float to the precision of dtype code `c` (f32 is the identity).
 template <int C>
