@@ -4,8 +4,8 @@
 //
 // A [M, K] and B [N, K] are E4M3 codes, both K-major (the reference's TN layout);
 // sa / sb are E8M0 scales in the 32_4_4 swizzled layout, fed to the MFMA's scale
-// operands directly (no dequantization): the four scales of a row for one 128-wide
-// K step are one aligned 32-bit word, and the MFMA's opsel picks the byte.
+// operands directly (no dequantization): the four scales of a row for a 128-wide K
+// block are one aligned 32-bit word, and the MFMA's opsel picks the byte.
 //
 // MFMA operand layout (measured on gfx950): lane l = 32*h + r holds row r; its bytes
 // 0..15 are k = 16h..16h+15 and bytes 16..31 are k = 32+16h..32+16h+15 of the 64-wide
@@ -15,27 +15,24 @@
 // consecutive output columns of one output row.
 //
 // Tiling: a 256-thread workgroup computes a 256 (m) x 256 (n) tile; its 4 waves each
-// own 128 x 128 = 4 x 4 MFMA tiles (256 fp32 accumulators per lane).  K advances 128
-// per stage through two LDS buffers (2 x 64 KB).  Global data goes straight to LDS
-// with buffer_load_dwordx4 ... lds (no VGPR staging): lane i of a load fills LDS
-// bytes [base + 16 i, base + 16 i + 16), so each lane fetches the global chunk that
-// belongs at its slot.  Rows past M / N and columns past K lie outside the buffer
-// descriptor's range and arrive as zeros.
+// own 128 x 128 = 4 x 4 MFMA tiles (256 fp32 accumulators per lane).  K advances 64
+// per stage (one MFMA K-step, 16 MFMAs per wave) through 4 LDS buffers of 34 KB.
+// Global data goes straight to LDS with buffer_load_dwordx4 ... lds (no VGPR
+// staging): lane i of a load fills LDS bytes [base + 16 i, base + 16 i + 16), so each
+// lane fetches the global chunk that belongs at its slot.  Rows past M / N, columns
+// past K and stages past the end lie outside the buffer descriptors' ranges and
+// arrive as zeros, so every stage runs the same branch-free code.
 //
-// LDS rows are 128 bytes; logical 16-byte chunk c of row r lives at chunk
-// c ^ (r & 7) ^ ((r >> 3) & 1): any 8 consecutive rows use 8 distinct bank groups and
-// any 16 split 8/8 over both halves of a 256-byte bank row, so fragment reads (32
-// rows at one chunk) are conflict-free for 32- or 64-bank LDS (0 conflicts measured).
+// Pipeline: at stage t (after its barrier) the fragments of t are already in
+// registers, so buffer t%4 is free and receives the loads of stage t+4; the LDS
+// reads of stage t+1's fragments and scale words overlap stage t's 16 MFMAs.  The
+// barrier of stage t waits only until this wave's loads of stage t+1 have landed
+// (vmcnt <= 20: the 10 loads each of stages t+2 and t+3 stay in flight), giving the
+// global loads three stages (~3000 MFMA cycles) of latency cover.
 //
-// Schedule per K stage (one barrier per stage):
-//   phase A: 16 MFMAs on fragments F0 (K-substep 0), interleaved with the LDS reads
-//            of F1 (substep 1);
-//   wait for this wave's LDS reads and stage loads, barrier;
-//   phase B: 16 MFMAs on F1, interleaved with the global->LDS loads of stage s+2 into
-//            the buffer just finished and the LDS reads of F0 and of the scale words
-//            of the next stage.
-// The E8M0 scale words travel through LDS as well (1 KB per operand per stage), so no
-// global load result is ever waited on inside the loop except at the stage barrier.
+// LDS rows are 64 bytes; logical 16-byte chunk c of row r lives at chunk
+// c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), which makes a 32-row fragment read (one chunk
+// of 32 consecutive rows) conflict-free for both 32- and 64-bank LDS layouts.
 // Workgroups are dispatched round-robin over the 8 XCDs; the tile index is remapped
 // so each XCD walks a contiguous range of tiles (column-major over m), keeping the
 // tiles that share a weight panel on one L2.
@@ -51,17 +48,43 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int BM = 256, BN = 256, BK = 128, NT = 256;
-constexpr int TILE = 256 * BK;   // bytes of one operand tile per stage
-constexpr int STILE = 1024;      // bytes of one operand's scale words per stage (256 rows)
+constexpr int BM = 256, BN = 256, BK = 64, NT = 256, NBUF = 4;
+constexpr int TILE = 256 * BK;  // bytes of one operand tile per stage (16 KB)
+constexpr int STILE = 1024;     // bytes of one operand's scale words per stage (256 rows)
+constexpr int LOADS_PER_STAGE = 10;  // per wave: 4 + 4 data, 2 scale DMA loads
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt [6:4],
+// lgkmcnt [11:8].  expcnt is left unconstrained (7).
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | ((vm >> 4) << 14); }
+
+// Workgroup barrier after an explicit s_waitcnt.  __syncthreads() would add a release
+// fence, i.e. vmcnt(0), draining the prefetched stages; here each wave has already
+// waited for exactly what the barrier must publish (its DMA loads of the next stage,
+// its LDS reads of the buffer about to be refilled), LDS is one coherent array per CU,
+// and the empty asm statements keep the compiler from moving memory operations across.
+template <int WAITCNT>
+__device__ __forceinline__ void stage_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAITCNT);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
 
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
 constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
 
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
+// Buffer descriptor over [p, p + bytes).  The inputs are wave-uniform by construction;
+// reading them through readfirstlane keeps the descriptor in SGPRs (a descriptor the
+// compiler believes divergent turns every load into a per-lane loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* up = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(up, 0, static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
+                                             0x00020000);
 }
 
 struct Args {
@@ -77,49 +100,42 @@ struct Args {
     int tiles_m, tiles_n;
 };
 
-// Per-lane state for the direct-to-LDS loads of one operand.  Wave w, load j (0..7)
-// covers tile rows R = 64 w + 8 j .. +7; lane i fills row R + i/8, physical chunk
-// i%8, i.e. logical chunk (i%8) ^ (i/8) ^ (j&1).
+// Direct-to-LDS loads of one operand.  Wave w, load j (0..3) covers tile rows
+// R = 64 w + 16 j .. +15 (1 KB of LDS); lane i fills row R + i/4, physical chunk i%4,
+// which holds logical chunk (i%4) ^ swz(row), and swz(row) depends only on i.
 struct Loader {
     __amdgpu_buffer_rsrc_t rs;
-    uint32_t base[2];  // byte offset of the lane's chunk for even / odd j, tile-relative, k0 = 0
-    int cbyte[2];      // the lane's chunk column in bytes (0..112) for even / odd j
-    uint32_t rowstep;  // 8 * K: byte distance between consecutive loads j
+    uint32_t base;     // lane's byte offset within rows R.. (k0 = 0)
+    int cbyte;         // lane's chunk column in bytes (0..48)
+    uint32_t rowstep;  // 16 * K: byte distance between consecutive loads j
     uint32_t row0;     // 64 * wave * K
 };
 
 __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int K, int wave, int lane) {
     Loader L;
-    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(valid_rows) * K);
-    const int rin = lane >> 3, pc = lane & 7;
-    L.cbyte[0] = (pc ^ rin) << 4;
-    L.cbyte[1] = (pc ^ rin ^ 1) << 4;
-    L.base[0] = static_cast<uint32_t>(rin * K + L.cbyte[0]);
-    L.base[1] = static_cast<uint32_t>(rin * K + L.cbyte[1]);
-    L.rowstep = 8u * K;
+    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * K);
+    const int row = lane >> 2;  // row within a 16-row load (R is a multiple of 16)
+    L.cbyte = ((lane & 3) ^ swz(row)) << 4;
+    L.base = static_cast<uint32_t>(row * K + L.cbyte);
+    L.rowstep = 16u * K;
     L.row0 = 64u * wave * K;
     return L;
 }
 
-// Issue the 8 global->LDS loads of one operand for the stage starting at k0.  A chunk
-// past the end of the row (last stage when K % 128 != 0) gets an offset outside the
-// descriptor and is written as zeros.
 __device__ __forceinline__ void issue_stage(const Loader& L, uint8_t* lds_tile, int wave, int k0, int K) {
+    const uint32_t add = (k0 + L.cbyte < K) ? static_cast<uint32_t>(k0) : 0x80000000u;  // past K: zeros
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        uint32_t off = L.base[j & 1] + L.row0 + j * L.rowstep + k0;
-        off = (k0 + L.cbyte[j & 1] < K) ? off : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(lds_tile + (64 * wave + 8 * j) * BK), 16, off, 0, 0,
-                                                 0);
-    }
+    for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(lds_tile + (64 * wave + 16 * j) * BK), 16,
+                                                 L.base + L.row0 + j * L.rowstep + add, 0, 0, 0);
 }
 
-// Scale words of a stage: for a 256-row tile and one 128-wide K step they are two
-// contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127, block column
-// k0/128), chunk (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand
-// w >> 1 (0 = weight, 1 = activation) to LDS with two 4-byte-per-lane DMA loads;
-// inside a chunk row r's word sits at (r % 32) * 16 + ((r % 128) / 32) * 4, so a
-// lane's words for its four 32-row tiles are one contiguous 16-byte LDS read.
+// Scale words of a stage: for a 256-row tile and one 128-wide K block they are two
+// contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
+// (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand w >> 1 (0 = weight,
+// 1 = activation) with two 4-byte-per-lane DMA loads.  Inside a chunk row r's word
+// sits at (r % 32) * 16 + ((r % 128) / 32) * 4, so a lane's words for its four 32-row
+// tiles are one contiguous 16-byte LDS read.
 __device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a, int rb0_b,
                                              int rb0_a, int ncb, int k0, int K, uint8_t* lds_stage, int wave,
                                              int lane) {
@@ -137,40 +153,35 @@ struct Frags {
     v8i a[4];  // activation fragments (MFMA operand 1)
 };
 
-// Byte offsets (within an operand tile) of this lane's two 16-byte halves of a fragment
-// for K-substep kk; tile t adds t * 32 rows = t * 4096 bytes.
+// Byte offsets (within an operand tile) of this lane's two 16-byte fragment halves
+// (chunks h and 2 + h); tile t adds t * 32 rows = t * 2048 bytes.
 struct FragAddr {
-    uint32_t lo[2], hi[2];  // [kk]
+    uint32_t lo, hi;
 };
 
 __device__ __forceinline__ FragAddr make_frag_addr(int row_base, int lane) {
     const int half = lane >> 5, r32 = lane & 31;
     const int row = row_base + r32;
     const int s = swz(row);
-    FragAddr f;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-        f.lo[kk] = static_cast<uint32_t>(row * BK + (((4 * kk + half) ^ s) << 4));
-        f.hi[kk] = static_cast<uint32_t>(row * BK + (((4 * kk + 2 + half) ^ s) << 4));
-    }
-    return f;
+    return FragAddr{static_cast<uint32_t>(row * BK + ((half ^ s) << 4)),
+                    static_cast<uint32_t>(row * BK + (((2 + half) ^ s) << 4))};
 }
 
-__device__ __forceinline__ v8i read_frag(const uint8_t* tile, uint32_t lo, uint32_t hi) {
-    const v4u x = *reinterpret_cast<const v4u*>(tile + lo);
-    const v4u y = *reinterpret_cast<const v4u*>(tile + hi);
-    v8i f;
-    f[0] = x[0]; f[1] = x[1]; f[2] = x[2]; f[3] = x[3];
-    f[4] = y[0]; f[5] = y[1]; f[6] = y[2]; f[7] = y[3];
-    return f;
+__device__ __forceinline__ v8i read_frag(const uint8_t* tile, const FragAddr& f) {
+    const v4u x = *reinterpret_cast<const v4u*>(tile + f.lo);
+    const v4u y = *reinterpret_cast<const v4u*>(tile + f.hi);
+    v8i r;
+    r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3];
+    r[4] = y[0]; r[5] = y[1]; r[6] = y[2]; r[7] = y[3];
+    return r;
 }
 
-__device__ __forceinline__ void read_frags(Frags& F, const uint8_t* tb, const uint8_t* ta, const FragAddr& fb,
-                                           const FragAddr& fa, int kk) {
+__device__ __forceinline__ void read_frags(Frags& F, const uint8_t* stage_buf, const FragAddr& fb,
+                                           const FragAddr& fa) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        F.b[t] = read_frag(tb + t * 32 * BK, fb.lo[kk], fb.hi[kk]);
-        F.a[t] = read_frag(ta + t * 32 * BK, fa.lo[kk], fa.hi[kk]);
+        F.b[t] = read_frag(stage_buf + t * 32 * BK, fb);
+        F.a[t] = read_frag(stage_buf + TILE + t * 32 * BK, fa);
     }
 }
 
@@ -212,12 +223,12 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 
 template <int OUT, int BIAS>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
-    // One LDS array per buffer parity, so the compiler can prove that the DMA writes of
-    // one stage never alias the fragment reads of the other and waits only at barriers.
-    __shared__ __attribute__((aligned(1024))) uint8_t smem0[2 * TILE];  // [weight, act][TILE]
-    __shared__ __attribute__((aligned(1024))) uint8_t smem1[2 * TILE];
-    __shared__ __attribute__((aligned(16))) uint8_t sscale0[2 * STILE];  // [weight, act][1 KB]
-    __shared__ __attribute__((aligned(16))) uint8_t sscale1[2 * STILE];
+    // One LDS array per buffer, indexed at compile time, so the compiler can prove the
+    // in-flight DMA writes never alias the fragment reads and adds no waits of its own.
+    __shared__ __attribute__((aligned(1024))) uint8_t buf0[2 * TILE + 2 * STILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t buf1[2 * TILE + 2 * STILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t buf2[2 * TILE + 2 * STILE];
+    __shared__ __attribute__((aligned(1024))) uint8_t buf3[2 * TILE + 2 * STILE];
 
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -245,19 +256,21 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
 
-    auto buf = [&](auto par_c) -> uint8_t* { return decltype(par_c)::value ? smem1 : smem0; };
-    auto sbuf = [&](auto par_c) -> uint8_t* { return decltype(par_c)::value ? sscale1 : sscale0; };
-    auto issue = [&](auto par_c, int s) {
-        uint8_t* b = buf(par_c);
+    auto buf = [&](auto b_c) -> uint8_t* {
+        constexpr int B = decltype(b_c)::value & 3;
+        return B == 0 ? buf0 : B == 1 ? buf1 : B == 2 ? buf2 : buf3;
+    };
+    auto issue = [&](auto b_c, int s) {
+        uint8_t* b = buf(b_c);
         issue_stage(LB, b, wave, s * BK, p.K);
         issue_stage(LA, b + TILE, wave, s * BK, p.K);
-        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, sbuf(par_c), wave, lane);
+        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, b + 2 * TILE, wave, lane);
     };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
-    // byte 0 / byte 2 are the lane-half's scales for K-substeps 0 / 1
+    // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
     const int hs = 8 * half;
-    auto read_scales = [&](auto par_c, uint32_t (&sb)[4], uint32_t (&sa)[4]) {
-        const uint8_t* st = sbuf(par_c);
+    auto read_scales = [&](auto b_c, uint32_t (&sb)[4], uint32_t (&sa)[4]) {
+        const uint8_t* st = buf(b_c) + 2 * TILE;
         const v4u wb = *reinterpret_cast<const v4u*>(st + wn * 512 + r32 * 16);
         const v4u wa = *reinterpret_cast<const v4u*>(st + STILE + wm * 512 + r32 * 16);
 #pragma unroll
@@ -269,59 +282,53 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
     uint32_t scb[4], sca[4];
     Frags F0, F1;
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
 
-    // One K stage held in buffer PAR: the stage's MFMAs, the reads of the next stage's
-    // F0 and scale words, and the loads of the stage after next into this buffer.  Every
-    // stage runs the same branch-free body; stages at or past K load as zeros, so the
-    // stage count is padded to even and the loop needs no tail variants.
-    auto stage = [&](auto par_c, int kt) {
-        using Other = std::integral_constant<int, 1 - decltype(par_c)::value>;
-        const uint8_t* tb = buf(par_c);
-        const uint8_t* ta = tb + TILE;
-        // ---- phase A: MFMAs on F0, LDS reads of F1
-        read_frags(F1, tb, ta, fab, faa, 1);
-        mfma16<0>(acc, F0, scb, sca);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
-        }
-        // stage kt+1 resident everywhere; every wave done reading stage kt
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        // ---- phase B: MFMAs on F1, loads of stage kt+2, LDS reads of F0 (stage kt+1)
+    // Stage t held in buffer B = t % 4 (compile-time): fragments F (stage t) are in
+    // registers; read stage t+1 into G while issuing stage t+4 into buffer B.
+    auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
+        constexpr int B = decltype(b_c)::value;
+        using Next = std::integral_constant<int, (B + 1) & 3>;
+        stage_barrier<waitcnt_vm_lgkm0(2 * LOADS_PER_STAGE)>();
         uint32_t nb[4], na[4];
-        issue(par_c, kt + 2);
-        read_frags(F0, buf(Other{}), buf(Other{}) + TILE, fab, faa, 0);
-        read_scales(Other{}, nb, na);
-        mfma16<2>(acc, F1, scb, sca);
+        issue(b_c, t + NBUF);
+        read_frags(G, buf(Next{}), fab, faa);
+        read_scales(Next{}, nb, na);
+        if constexpr ((B & 1) == 0) mfma16<0>(acc, F, scb, sca);
+        else mfma16<2>(acc, F, scb, sca);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 1, 0);
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            scb[t] = nb[t];
-            sca[t] = na[t];
+        for (int i = 0; i < 4; ++i) {
+            scb[i] = nb[i];
+            sca[i] = na[i];
         }
     };
 
-    // prologue: stage 0 resident, stage 1 in flight, F0 and stage-0 scales read
-    issue(P0{}, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    issue(P1{}, 1);
-    read_frags(F0, smem0, smem0 + TILE, fab, faa, 0);
-    read_scales(P0{}, scb, sca);
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    using B3 = std::integral_constant<int, 3>;
 
-    // stages in pairs: even stages in buffer 0, odd in buffer 1
-    for (int kt = 0; kt < KT; kt += 2) {
-        stage(P0{}, kt);
-        stage(P1{}, kt + 1);
+    // prologue: stages 0..3 in flight, stage 0 resident and read
+    issue(B0{}, 0);
+    issue(B1{}, 1);
+    issue(B2{}, 2);
+    issue(B3{}, 3);
+    stage_barrier<waitcnt_vm_lgkm0(3 * LOADS_PER_STAGE)>();
+    read_frags(F0, buf0, fab, faa);
+    read_scales(B0{}, scb, sca);
+
+    // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
+    for (int t = 0; t < KT; t += 4) {
+        stage(B0{}, t, F0, F1);
+        stage(B1{}, t + 1, F1, F0);
+        stage(B2{}, t + 2, F0, F1);
+        stage(B3{}, t + 3, F1, F0);
     }
     __builtin_amdgcn_s_waitcnt(0);  // drain the loads issued past the last stage
 
