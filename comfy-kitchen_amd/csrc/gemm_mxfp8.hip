@@ -17,18 +17,19 @@
 // Tiling: a 256-thread workgroup computes a 256 (m) x 256 (n) tile; its 4 waves each
 // own 128 x 128 = 4 x 4 MFMA tiles (256 fp32 accumulators per lane).  K advances 64
 // per stage (one MFMA K-step, 16 MFMAs per wave) through 4 LDS buffers of 34 KB.
-// Global data goes straight to LDS with buffer_load_dwordx4 ... lds (no VGPR
-// staging): lane i of a load fills LDS bytes [base + 16 i, base + 16 i + 16), so each
-// lane fetches the global chunk that belongs at its slot.  Rows past M / N, columns
-// past K and stages past the end lie outside the buffer descriptors' ranges and
-// arrive as zeros, so every stage runs the same branch-free code.
+// Rows past M / N, columns past K and stages past the end lie outside the buffer
+// descriptors' ranges and load as zeros, so every stage runs the same branch-free code.
 //
 // Pipeline: at stage t (after its barrier) the fragments of t are already in
-// registers, so buffer t%4 is free and receives the loads of stage t+4; the LDS
-// reads of stage t+1's fragments and scale words overlap stage t's 16 MFMAs.  The
-// barrier of stage t waits only until this wave's loads of stage t+1 have landed
-// (vmcnt <= 20: the 10 loads each of stages t+2 and t+3 stay in flight), giving the
-// global loads three stages (~3000 MFMA cycles) of latency cover.
+// registers; the LDS reads of stage t+1's fragments and scale words overlap stage t's
+// 16 MFMAs.  Global data moves in pairs of stages through registers: one load
+// instruction brings whole 128-byte lines (both stages' halves of 8 rows), and an even
+// stage t writes the staged pair t+2, t+3 to LDS and loads t+4, t+5, so loads have two
+// stages (~2000 MFMA cycles) to arrive.  Register staging rather than direct-to-LDS
+// loads because each buffer_load ... lds instruction holds up the issuing wave's MFMA
+// stream for ~22 cycles on gfx950, while plain loads and ds_writes hide under the MFMAs.
+// Each barrier waits for LDS traffic only; the compiler's vmcnt waits guard the staged
+// registers.
 //
 // LDS rows are 64 bytes; logical 16-byte chunk c of row r lives at chunk
 // c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), which makes a 32-row fragment read (one chunk
@@ -46,22 +47,24 @@ namespace mx {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 256, NBUF = 4;
 constexpr int TILE = 256 * BK;  // bytes of one operand tile per stage (16 KB)
 constexpr int STILE = 1024;     // bytes of one operand's scale words per stage (256 rows)
-constexpr int LOADS_PER_STAGE = 10;  // per wave: 4 + 4 data, 2 scale DMA loads
+constexpr int BUF = 2 * TILE + 2 * STILE;  // one stage buffer: weight tile, activation tile, scales
+constexpr int EPI_ROW = 528;         // bytes of one staged 16-bit output row (512 + 16 pad)
+static_assert(64 * EPI_ROW <= BUF, "an output slab must fit one stage buffer");
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt [6:4],
 // lgkmcnt [11:8].  expcnt is left unconstrained (7).
 constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | ((vm >> 4) << 14); }
+constexpr int WAIT_LGKM0 = waitcnt_vm_lgkm0(63);  // LDS only; global loads stay in flight
 
 // Workgroup barrier after an explicit s_waitcnt.  __syncthreads() would add a release
 // fence, i.e. vmcnt(0), draining the prefetched stages; here each wave has already
-// waited for exactly what the barrier must publish (its DMA loads of the next stage,
-// its LDS reads of the buffer about to be refilled), LDS is one coherent array per CU,
-// and the empty asm statements keep the compiler from moving memory operations across.
+// waited for exactly what the barrier must publish (its LDS writes and reads), LDS is
+// one coherent array per CU, and the empty asm statements keep the compiler from
+// moving memory operations across.
 template <int WAITCNT>
 __device__ __forceinline__ void stage_barrier() {
     __asm__ volatile("" ::: "memory");
@@ -71,7 +74,7 @@ __device__ __forceinline__ void stage_barrier() {
 }
 
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
-constexpr int SG_MFMA = 0x008, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
+constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
 
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
@@ -100,52 +103,74 @@ struct Args {
     int tiles_m, tiles_n;
 };
 
-// Direct-to-LDS loads of one operand.  Wave w, load j (0..3) covers tile rows
-// R = 64 w + 16 j .. +15 (1 KB of LDS); lane i fills row R + i/4, physical chunk i%4,
-// which holds logical chunk (i%4) ^ swz(row), and swz(row) depends only on i.
+// Register-staged loads of one operand for a pair of stages (s, s + 1), i.e. K bytes
+// [k0, k0 + 128) of the tile's 256 rows.  Wave w, load j (0..7) covers rows
+// R = 64 w + 8 j .. +7: lane i fetches 16-byte chunk c = i % 8 of row R + i / 8, so each
+// 8 lanes read one whole 128-byte line (with all CUs loading, half-line requests reach
+// only ~70% of the L2 throughput of whole lines).  Chunks 0..3 go to stage s's buffer,
+// 4..7 to stage s + 1's, at physical chunk (c % 4) ^ swz(row); swz(row + 8) = swz(row) ^ 1.
 struct Loader {
     __amdgpu_buffer_rsrc_t rs;
-    uint32_t base;     // lane's byte offset within rows R.. (k0 = 0)
-    int cbyte;         // lane's chunk column in bytes (0..48)
-    uint32_t rowstep;  // 16 * K: byte distance between consecutive loads j
-    uint32_t row0;     // 64 * wave * K
+    uint32_t voff;      // lane's global byte offset for j = 0, k0 = 0
+    uint32_t rowstep;   // 8 * K: global distance between consecutive loads j
+    int cbyte;          // 16 * c
+    uint32_t lds_even;  // lane's LDS offset within a stage tile for j = 0 (even j adds 512 j)
+    uint32_t lds_odd;   // the same for odd j (before adding 512 j)
+    bool hi;            // chunk belongs to stage s + 1
 };
 
 __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int K, int wave, int lane) {
     Loader L;
     L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * K);
-    const int row = lane >> 2;  // row within a 16-row load (R is a multiple of 16)
-    L.cbyte = ((lane & 3) ^ swz(row)) << 4;
-    L.base = static_cast<uint32_t>(row * K + L.cbyte);
-    L.rowstep = 16u * K;
-    L.row0 = 64u * wave * K;
+    const int row = 64 * wave + (lane >> 3), c = lane & 7;
+    L.cbyte = c << 4;
+    L.voff = static_cast<uint32_t>(row * K + L.cbyte);
+    L.rowstep = 8u * K;
+    L.lds_even = static_cast<uint32_t>(row * BK + (((c & 3) ^ swz(row)) << 4));
+    L.lds_odd = static_cast<uint32_t>(row * BK + (((c & 3) ^ swz(row) ^ 1) << 4));
+    L.hi = c >= 4;
     return L;
 }
 
-__device__ __forceinline__ void issue_stage(const Loader& L, uint8_t* lds_tile, int wave, int k0, int K) {
+__device__ __forceinline__ void load_pair(const Loader& L, v4u (&x)[8], int k0, int K) {
     const uint32_t add = (k0 + L.cbyte < K) ? static_cast<uint32_t>(k0) : 0x80000000u;  // past K: zeros
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(lds_tile + (64 * wave + 16 * j) * BK), 16,
-                                                 L.base + L.row0 + j * L.rowstep + add, 0, 0, 0);
+    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_raw_buffer_load_b128(L.rs, L.voff + j * L.rowstep + add, 0, 0);
 }
 
-// Scale words of a stage: for a 256-row tile and one 128-wide K block they are two
-// contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
+__device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], uint8_t* tx, uint8_t* ty) {
+    uint8_t* t = L.hi ? ty : tx;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<v4u*>(t + ((j & 1) ? L.lds_odd : L.lds_even) + 512 * j) = x[j];
+}
+
+// Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
+// two contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
 // (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand w >> 1 (0 = weight,
-// 1 = activation) with two 4-byte-per-lane DMA loads.  Inside a chunk row r's word
-// sits at (r % 32) * 16 + ((r % 128) / 32) * 4, so a lane's words for its four 32-row
-// tiles are one contiguous 16-byte LDS read.
-__device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a, int rb0_b,
-                                             int rb0_a, int ncb, int k0, int K, uint8_t* lds_stage, int wave,
-                                             int lane) {
+// 1 = activation), 2 words per lane.  Inside a chunk row r's word sits at
+// (r % 32) * 16 + ((r % 128) / 32) * 4, so a lane's words for its four 32-row tiles are
+// one contiguous 16-byte LDS read.  Both stages of the pair get a copy.
+struct ScaleWords {
+    uint32_t s0, s1;
+};
+
+__device__ __forceinline__ void load_scales(ScaleWords& S, __amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a,
+                                            int rb0_b, int rb0_a, int ncb, int k0, int K, int wave, int lane) {
     const int op = wave >> 1, rb = wave & 1;
     const __amdgpu_buffer_rsrc_t rs = op ? rs_a : rs_b;
     uint32_t chunk = static_cast<uint32_t>(((op ? rb0_a : rb0_b) + rb) * ncb + (k0 >> 7)) * 512u;
     chunk = k0 < K ? chunk : 0x80000000u;  // stages past K: zero scale words
-    uint8_t* dst = lds_stage + op * STILE + rb * 512;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 4, chunk + lane * 4, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 256), 4, chunk + 256 + lane * 4, 0, 0, 0);
+    S.s0 = __builtin_amdgcn_raw_buffer_load_b32(rs, chunk + lane * 4, 0, 0);
+    S.s1 = __builtin_amdgcn_raw_buffer_load_b32(rs, chunk + 256 + lane * 4, 0, 0);
+}
+
+__device__ __forceinline__ void store_scales(const ScaleWords& S, uint8_t* sx, uint8_t* sy, int wave, int lane) {
+    const int off = (wave >> 1) * STILE + (wave & 1) * 512 + lane * 4;
+    *reinterpret_cast<uint32_t*>(sx + off) = S.s0;
+    *reinterpret_cast<uint32_t*>(sx + off + 256) = S.s1;
+    *reinterpret_cast<uint32_t*>(sy + off) = S.s0;
+    *reinterpret_cast<uint32_t*>(sy + off + 256) = S.s1;
 }
 
 struct Frags {
@@ -223,12 +248,8 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 
 template <int OUT, int BIAS>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
-    // One LDS array per buffer, indexed at compile time, so the compiler can prove the
-    // in-flight DMA writes never alias the fragment reads and adds no waits of its own.
-    __shared__ __attribute__((aligned(1024))) uint8_t buf0[2 * TILE + 2 * STILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t buf1[2 * TILE + 2 * STILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t buf2[2 * TILE + 2 * STILE];
-    __shared__ __attribute__((aligned(1024))) uint8_t buf3[2 * TILE + 2 * STILE];
+    // the stage buffers, one array so per-lane LDS addresses differ only by immediates
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[NBUF * BUF];
 
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -258,14 +279,22 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
     auto buf = [&](auto b_c) -> uint8_t* {
         constexpr int B = decltype(b_c)::value & 3;
-        return B == 0 ? buf0 : B == 1 ? buf1 : B == 2 ? buf2 : buf3;
+        return lds + B * BUF;
     };
-    auto issue = [&](auto b_c, int s) {
-        uint8_t* b = buf(b_c);
-        issue_stage(LB, b, wave, s * BK, p.K);
-        issue_stage(LA, b + TILE, wave, s * BK, p.K);
-        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, b + 2 * TILE, wave, lane);
+    // Register staging: a pair of stages of one operand (+ the pair's scale words with
+    // the weight) at a time.
+    v4u SB[8], SA[8];
+    ScaleWords SW;
+    auto load_b = [&](int s) {
+        load_pair(LB, SB, s * BK, p.K);
+        load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
     };
+    auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
+    auto store_b = [&](auto x_c, auto y_c) {
+        store_pair(LB, SB, buf(x_c), buf(y_c));
+        store_scales(SW, buf(x_c) + 2 * TILE, buf(y_c) + 2 * TILE, wave, lane);
+    };
+    auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
     const int hs = 8 * half;
@@ -284,23 +313,41 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     Frags F0, F1;
 
     // Stage t held in buffer B = t % 4 (compile-time): fragments F (stage t) are in
-    // registers; read stage t+1 into G while issuing stage t+4 into buffer B.
+    // registers; read stage t+1 into G.  A pair of stages (s, s+1), s even, moves in
+    // two halves: the activation pair is loaded at stage s-4 and written to LDS at
+    // s-3, the weight pair (with scales) loaded at s-3 and written at s-2.  Each write
+    // targets buffers whose previous stages were read before the current barrier, and
+    // each staged half has one stage to arrive.
     auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
         constexpr int B = decltype(b_c)::value;
         using Next = std::integral_constant<int, (B + 1) & 3>;
-        stage_barrier<waitcnt_vm_lgkm0(2 * LOADS_PER_STAGE)>();
+        using P2 = std::integral_constant<int, (B + 2) & 3>;
+        using P3 = std::integral_constant<int, (B + 3) & 3>;
+        stage_barrier<WAIT_LGKM0>();
         uint32_t nb[4], na[4];
-        issue(b_c, t + NBUF);
         read_frags(G, buf(Next{}), fab, faa);
         read_scales(Next{}, nb, na);
-        if constexpr ((B & 1) == 0) mfma16<0>(acc, F, scb, sca);
-        else mfma16<2>(acc, F, scb, sca);
+        if constexpr ((B & 1) == 0) {
+            store_b(P2{}, P3{});  // stages t+2, t+3
+            load_a(t + 4);
+            mfma16<0>(acc, F, scb, sca);
+        } else {
+            store_a(P3{}, b_c);  // stages t+3, t+4
+            load_b(t + 3);
+            mfma16<2>(acc, F, scb, sca);
+        }
+        // fragment reads under the first 9 MFMAs, LDS writes and global loads under the
+        // last 7
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < 9; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
             __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
             __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 2, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -314,13 +361,16 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     using B2 = std::integral_constant<int, 2>;
     using B3 = std::integral_constant<int, 3>;
 
-    // prologue: stages 0..3 in flight, stage 0 resident and read
-    issue(B0{}, 0);
-    issue(B1{}, 1);
-    issue(B2{}, 2);
-    issue(B3{}, 3);
-    stage_barrier<waitcnt_vm_lgkm0(3 * LOADS_PER_STAGE)>();
-    read_frags(F0, buf0, fab, faa);
+    // prologue: stages 0..3 resident except the weight half of 2, 3 (staged), stage 0 read
+    load_a(0);
+    load_b(0);
+    store_a(B0{}, B1{});
+    load_a(2);
+    store_b(B0{}, B1{});
+    load_b(2);
+    store_a(B2{}, B3{});
+    stage_barrier<WAIT_LGKM0>();
+    read_frags(F0, lds, fab, faa);
     read_scales(B0{}, scb, sca);
 
     // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
@@ -330,30 +380,79 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
         stage(B2{}, t + 2, F0, F1);
         stage(B3{}, t + 3, F1, F0);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // drain the loads issued past the last stage
+    // the epilogue reuses the LDS buffers
+    __syncthreads();
 
     // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
     // n = 8*g + 4*half (+0..3) of weight tile i.
+    if constexpr (OUT != CKH_F32) {
+        // 16-bit output: stage the tile in LDS as 256 rows of 512 bytes (padded to
+        // EPI_ROW so a fragment's 32 rows hit distinct banks), the 64-row slab q in
+        // buffer q, then store whole rows: 64 lanes x 16 bytes cover two rows.
+        auto slab = [&](int q) -> uint8_t* { return lds + q * BUF; };
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + r32;
-        if (m >= p.M) continue;
+        for (int j = 0; j < 4; ++j) {
+            uint8_t* rowp = slab(wm * 2 + (j >> 1)) + ((j & 1) * 32 + r32) * EPI_ROW;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int n = n0 + wn * 128 + i * 32 + 8 * g + 4 * half;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[e] = acc[i][j][4 * g + e] + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
-                const int64_t idx = static_cast<int64_t>(m) * p.N + n;
-                if (n + 3 < p.N && (p.N & 3) == 0) {
-                    store4<OUT>(p.out, idx, v);
-                } else {
+                for (int g = 0; g < 4; ++g) {
+                    const int nl = wn * 128 + i * 32 + 8 * g + 4 * half;
+                    const int n = n0 + nl;
+                    float v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (n + e < p.N) store1<OUT>(p.out, idx + e, v[e]);
+                        v[e] = acc[i][j][4 * g + e] + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
+                    uint32_t w0 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[0]) : f_to_f16(v[0])) |
+                                  ((OUT == CKH_BF16 ? f_to_bf16_rne(v[1]) : f_to_f16(v[1])) << 16);
+                    uint32_t w1 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[2]) : f_to_f16(v[2])) |
+                                  ((OUT == CKH_BF16 ? f_to_bf16_rne(v[3]) : f_to_f16(v[3])) << 16);
+                    *reinterpret_cast<uint2*>(rowp + nl * 2) = make_uint2(w0, w1);
+                }
+            }
+        }
+        __syncthreads();
+        const uint8_t* src = slab(wave);
+        const int c = lane & 31;
+        const int n = n0 + 8 * c;
+        const bool vec = (p.N & 7) == 0 && n + 8 <= p.N;
+#pragma unroll 4
+        for (int it = 0; it < 32; ++it) {
+            const int rl = 2 * it + (lane >> 5);
+            const int m = m0 + wave * 64 + rl;
+            const v4u d = *reinterpret_cast<const v4u*>(src + rl * EPI_ROW + c * 16);
+            if (m >= p.M) continue;
+            uint16_t* o = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m) * p.N + n;
+            if (vec) {
+                *reinterpret_cast<v4u*>(o) = d;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < p.N) o[e] = static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + wm * 128 + j * 32 + r32;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int n = n0 + wn * 128 + i * 32 + 8 * g + 4 * half;
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = acc[i][j][4 * g + e] + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
+                    const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+                    if (n + 3 < p.N && (p.N & 3) == 0) {
+                        store4<OUT>(p.out, idx, v);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) store1<OUT>(p.out, idx + e, v[e]);
+                    }
                 }
             }
         }
