@@ -38,6 +38,7 @@
 // so each XCD walks a contiguous range of tiles (column-major over m), keeping the
 // tiles that share a weight panel on one L2.
 #include <type_traits>
+#include <utility>
 
 #include "ckh_common.h"
 
@@ -48,11 +49,15 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, BN = 256, BK = 64, NT = 256, NBUF = 4;
+constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
 constexpr int TILE = 256 * BK;  // bytes of one operand tile per stage (16 KB)
 constexpr int STILE = 1024;     // bytes of one operand's scale words per stage (256 rows)
-constexpr int BUF = 2 * TILE + 2 * STILE;  // one stage buffer: weight tile, activation tile, scales
-constexpr int EPI_ROW = 528;         // bytes of one staged 16-bit output row (512 + 16 pad)
+// One stage buffer: weight tile, activation tile, scales, and 64 bytes of padding.  LDS
+// banks repeat every 128 bytes; a staged store writes row r of buffers s and s + 1
+// from 8 neighbouring lanes (64 bytes each), which the padding puts in opposite halves
+// of the bank cycle (measured conflict-free; without it every store conflicts 2-way).
+constexpr int BUF = 2 * TILE + 2 * STILE + 64;
+constexpr int EPI_ROW = 520;  // bytes of one staged 16-bit output row (512 + 8 pad)
 static_assert(64 * EPI_ROW <= BUF, "an output slab must fit one stage buffer");
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt [6:4],
@@ -73,8 +78,11 @@ __device__ __forceinline__ void stage_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
-// scheduling-group masks of __builtin_amdgcn_sched_group_barrier
-constexpr int SG_MFMA = 0x008, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200;
+// fn(integral_constant<int, K>) for each K in order
+template <typename Fn, int... K>
+__device__ __forceinline__ void for_each_index(Fn&& fn, std::integer_sequence<int, K...>) {
+    (fn(std::integral_constant<int, K>{}), ...);
+}
 
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
@@ -132,17 +140,42 @@ __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int vali
     return L;
 }
 
+// Offset added to a lane's global address for the pair at k0: past K the lane reads
+// zeros from outside the descriptor's range.
+__device__ __forceinline__ uint32_t pair_add(const Loader& L, int k0, int K) {
+    return (k0 + L.cbyte < K) ? static_cast<uint32_t>(k0) : 0x80000000u;
+}
+
+template <int J>
+__device__ __forceinline__ void load_piece(const Loader& L, v4u (&x)[8], uint32_t add) {
+    x[J] = __builtin_amdgcn_raw_buffer_load_b128(L.rs, L.voff + J * L.rowstep + add, 0, 0);
+}
+
+template <int J>
+__device__ __forceinline__ void store_piece(const Loader& L, const v4u (&x)[8], uint8_t* tx, uint8_t* ty) {
+    uint8_t* t = L.hi ? ty : tx;
+    *reinterpret_cast<v4u*>(t + ((J & 1) ? L.lds_odd : L.lds_even) + 512 * J) = x[J];
+}
+
+template <int... J>
+__device__ __forceinline__ void load_pair(const Loader& L, v4u (&x)[8], int k0, int K,
+                                          std::integer_sequence<int, J...>) {
+    const uint32_t add = pair_add(L, k0, K);
+    (load_piece<J>(L, x, add), ...);
+}
+
 __device__ __forceinline__ void load_pair(const Loader& L, v4u (&x)[8], int k0, int K) {
-    const uint32_t add = (k0 + L.cbyte < K) ? static_cast<uint32_t>(k0) : 0x80000000u;  // past K: zeros
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_raw_buffer_load_b128(L.rs, L.voff + j * L.rowstep + add, 0, 0);
+    load_pair(L, x, k0, K, std::make_integer_sequence<int, 8>{});
+}
+
+template <int... J>
+__device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], uint8_t* tx, uint8_t* ty,
+                                           std::integer_sequence<int, J...>) {
+    (store_piece<J>(L, x, tx, ty), ...);
 }
 
 __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], uint8_t* tx, uint8_t* ty) {
-    uint8_t* t = L.hi ? ty : tx;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<v4u*>(t + ((j & 1) ? L.lds_odd : L.lds_even) + 512 * j) = x[j];
+    store_pair(L, x, tx, ty, std::make_integer_sequence<int, 8>{});
 }
 
 // Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
@@ -248,8 +281,12 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 
 template <int OUT, int BIAS>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
-    // the stage buffers, one array so per-lane LDS addresses differ only by immediates
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[NBUF * BUF];
+    // Stage buffers 0, 1 and 2, 3 in two arrays.  Every stage reads fragments from one
+    // array and writes staged data into the other, so the compiler knows they never
+    // alias and may interleave the two freely; within an array, per-lane addresses of
+    // different buffers differ only by immediates.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
 
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -279,7 +316,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
     auto buf = [&](auto b_c) -> uint8_t* {
         constexpr int B = decltype(b_c)::value & 3;
-        return lds + B * BUF;
+        return (B < 2 ? lds01 : lds23) + (B & 1) * BUF;
     };
     // Register staging: a pair of stages of one operand (+ the pair's scale words with
     // the weight) at a time.
@@ -316,43 +353,67 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     // registers; read stage t+1 into G.  A pair of stages (s, s+1), s even, moves in
     // two halves: the activation pair is loaded at stage s-4 and written to LDS at
     // s-3, the weight pair (with scales) loaded at s-3 and written at s-2.  Each write
-    // targets buffers whose previous stages were read before the current barrier, and
-    // each staged half has one stage to arrive.
+    // targets buffers whose previous stages were read before the current barrier.
+    //
+    // The stage is scheduled by hand in 16 slots, one MFMA each (sched_barrier keeps
+    // the order): the next stage's scale words first (their shifts 12 slots later, so
+    // no LDS latency is exposed), then its fragments in the order the next stage uses
+    // them, and in slots 0..7 one staged chunk written to LDS followed by the load that
+    // refills its registers, which therefore has a whole stage to arrive.
     auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
         constexpr int B = decltype(b_c)::value;
+        constexpr bool EVEN = (B & 1) == 0;
+        constexpr int OPSEL = EVEN ? 0 : 2;
         using Next = std::integral_constant<int, (B + 1) & 3>;
         using P2 = std::integral_constant<int, (B + 2) & 3>;
         using P3 = std::integral_constant<int, (B + 3) & 3>;
         stage_barrier<WAIT_LGKM0>();
+        const uint8_t* nx = buf(Next{});
+        uint8_t* wx = EVEN ? buf(P2{}) : buf(P3{}) + TILE;
+        uint8_t* wy = EVEN ? buf(P3{}) : buf(b_c) + TILE;
+        const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, p.K) : pair_add(LB, (t + 3) * BK, p.K);
+        v4u wb, wa;
         uint32_t nb[4], na[4];
-        read_frags(G, buf(Next{}), fab, faa);
-        read_scales(Next{}, nb, na);
-        if constexpr ((B & 1) == 0) {
-            store_b(P2{}, P3{});  // stages t+2, t+3
-            load_a(t + 4);
-            mfma16<0>(acc, F, scb, sca);
-        } else {
-            store_a(P3{}, b_c);  // stages t+3, t+4
-            load_b(t + 3);
-            mfma16<2>(acc, F, scb, sca);
-        }
-        // fragment reads under the first 9 MFMAs, LDS writes and global loads under the
-        // last 7
+        auto slot = [&](auto k_c) {
+            constexpr int k = decltype(k_c)::value;
+            constexpr int i = k / 4, j = k % 4;
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.b[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
+                                                                        OPSEL, sca[j]);
+            if constexpr (k == 0) {
+                wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + wn * 512 + r32 * 16);
+                wa = *reinterpret_cast<const v4u*>(nx + 2 * TILE + STILE + wm * 512 + r32 * 16);
+            }
+            if constexpr (k == 1) G.a[0] = read_frag(nx + TILE, faa);
+            if constexpr (k == 2) G.b[0] = read_frag(nx, fab);
+            if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
+            if constexpr (k >= 6 && k <= 8) G.b[k - 5] = read_frag(nx + (k - 5) * 32 * BK, fab);
+            if constexpr (k < 8) {
+                if constexpr (EVEN) {
+                    store_piece<k>(LB, SB, wx, wy);
+                    load_piece<k>(LA, SA, add);
+                } else {
+                    store_piece<k>(LA, SA, wx, wy);
+                    load_piece<k>(LB, SB, add);
+                }
+            }
+            if constexpr (k == 8) {
+                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
+                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
+            }
+            if constexpr (k == 12) {
 #pragma unroll
-        for (int i = 0; i < 9; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_READ, 2, 0);
-        }
+                for (int u = 0; u < 4; ++u) {
+                    nb[u] = wb[u] >> hs;
+                    na[u] = wa[u] >> hs;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for_each_index(slot, std::make_integer_sequence<int, 16>{});
 #pragma unroll
-        for (int i = 0; i < 7; ++i) {
-            __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, 2, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            scb[i] = nb[i];
-            sca[i] = na[i];
+        for (int u = 0; u < 4; ++u) {
+            scb[u] = nb[u];
+            sca[u] = na[u];
         }
     };
 
@@ -370,7 +431,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     load_b(2);
     store_a(B2{}, B3{});
     stage_barrier<WAIT_LGKM0>();
-    read_frags(F0, lds, fab, faa);
+    read_frags(F0, lds01, fab, faa);
     read_scales(B0{}, scb, sca);
 
     // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
@@ -386,10 +447,11 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
     // n = 8*g + 4*half (+0..3) of weight tile i.
     if constexpr (OUT != CKH_F32) {
-        // 16-bit output: stage the tile in LDS as 256 rows of 512 bytes (padded to
-        // EPI_ROW so a fragment's 32 rows hit distinct banks), the 64-row slab q in
-        // buffer q, then store whole rows: 64 lanes x 16 bytes cover two rows.
-        auto slab = [&](int q) -> uint8_t* { return lds + q * BUF; };
+        // 16-bit output: stage the tile in LDS as 256 rows of 512 bytes, the 64-row slab
+        // q in buffer q.  The pitch EPI_ROW = 520 spreads the 32 rows of one fragment
+        // store over distinct bank pairs.  Then each wave stores whole rows of its slab:
+        // 64 lanes x 8 bytes per row.
+        auto slab = [&](int q) -> uint8_t* { return (q < 2 ? lds01 : lds23) + (q & 1) * BUF; };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint8_t* rowp = slab(wm * 2 + (j >> 1)) + ((j & 1) * 32 + r32) * EPI_ROW;
@@ -412,23 +474,22 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             }
         }
         __syncthreads();
-        const uint8_t* src = slab(wave);
-        const int c = lane & 31;
-        const int n = n0 + 8 * c;
-        const bool vec = (p.N & 7) == 0 && n + 8 <= p.N;
-#pragma unroll 4
-        for (int it = 0; it < 32; ++it) {
-            const int rl = 2 * it + (lane >> 5);
-            const int m = m0 + wave * 64 + rl;
-            const v4u d = *reinterpret_cast<const v4u*>(src + rl * EPI_ROW + c * 16);
-            if (m >= p.M) continue;
-            uint16_t* o = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m) * p.N + n;
+        const uint8_t* src = slab(wave) + lane * 8;
+        const int n = n0 + 4 * lane;
+        const bool vec = (p.N & 3) == 0 && n + 4 <= p.N;
+        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64) * p.N + n;
+        const int rows = min(64, p.M - (m0 + wave * 64));
+#pragma unroll 8
+        for (int rl = 0; rl < 64; ++rl) {
+            const uint2 d = *reinterpret_cast<const uint2*>(src + rl * EPI_ROW);
+            if (rl >= rows) break;
+            uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
             if (vec) {
-                *reinterpret_cast<v4u*>(o) = d;
+                *reinterpret_cast<uint2*>(o) = d;
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (n + e < p.N) o[e] = static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1)));
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < p.N) o[e] = static_cast<uint16_t>((e < 2 ? d.x : d.y) >> (16 * (e & 1)));
             }
         }
     } else {
