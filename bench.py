@@ -121,9 +121,21 @@ def _sets_for(bytes_per_set: int) -> int:
     return max(2, math.ceil(ROTATE_BYTES / max(bytes_per_set, 1)))
 
 
+SETTLE_S = 0.3
+
+
 def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> float:
-    """Average ms per call: `make_call(i)` returns a zero-arg launcher for buffer set i."""
+    """Average ms per call: `make_call(i)` returns a zero-arg launcher for buffer set i.
+
+    Before the W warmup calls the op runs for SETTLE_S seconds so the GPU leaves its
+    idle clock state (an MI355X ramps its clock over tens of milliseconds; timing a
+    freshly woken GPU understates kernels by up to ~15%)."""
     calls = [make_call(i) for i in range(n_sets)]
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for c in calls:
+            c()
+        torch.cuda.synchronize()
     for i in range(warmup):
         calls[i % n_sets]()
     torch.cuda.synchronize()
@@ -150,12 +162,13 @@ def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> f
     return start.elapsed_time(end) / steps
 
 
-def time_cpu(fn, min_reps=2, budget_s=8.0) -> tuple[float, int]:
-    """Median seconds per call of fn() on the CPU (bounded by budget_s after one warmup)."""
+def time_cpu(fn, min_reps=3, budget_s=3.0) -> tuple[float, int]:
+    """Median seconds per call of fn() on the CPU: repeated for budget_s (at least min_reps
+    calls) after one warmup call."""
     fn()
     ts = []
     t_all = time.perf_counter()
-    while len(ts) < min_reps or (time.perf_counter() - t_all < budget_s and len(ts) < 5):
+    while len(ts) < min_reps or time.perf_counter() - t_all < budget_s:
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
@@ -180,8 +193,9 @@ def load_traffic() -> dict:
     p = REPO / "profiles" / "traffic.json"
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("bytes_per_launch", {})
-        except (ValueError, OSError):
+            per = json.loads(p.read_text()).get("bytes_per_launch", {})
+            return {k: v.get("total") for k, v in per.items()}
+        except (ValueError, OSError, AttributeError):
             return {}
     return {}
 
@@ -206,14 +220,14 @@ def run_gpu(configs, steps, warmup, log):
         ms = time_graph(lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps, warmup,
                         check=lambda outs: [same(o, ref_q) or sys.exit("graph replay mismatch c1 q") for o in outs])
         res["quantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_per_tensor_fp8"], ms,
-                                                                      traffic.get("quantize_fp8"))}
+                                                                      traffic.get("quantize_per_tensor_fp8"))}
         log(f"c1 quantize_per_tensor_fp8: {ms * 1e3:.2f} us")
         qs = [ref_q.clone() for _ in range(nset)]
         ref_dq = ck.dequantize_per_tensor_fp8(ref_q, scale)
         ms = time_graph(lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
                         check=lambda outs: [same(o, ref_dq) or sys.exit("graph replay mismatch c1 dq") for o in outs])
         res["dequantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_per_tensor_fp8"], ms,
-                                                                        traffic.get("dequantize_fp8"))}
+                                                                        traffic.get("dequantize_per_tensor_fp8"))}
         log(f"c1 dequantize_per_tensor_fp8: {ms * 1e3:.2f} us")
         del xs, qs
 
@@ -249,8 +263,11 @@ def run_gpu(configs, steps, warmup, log):
             qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
             try:
                 ref = ck.scaled_mm_mxfp8(qa, qw, sa, sw)
-                ms = time_graph(lambda i: (lambda: ck.scaled_mm_mxfp8(qa, qw, sa, sw)), 2, max(steps // 4, 5),
+                nset = _sets_for(qa.numel() + qw.numel())
+                ops_ = [(qa.clone(), qw.clone(), sa.clone(), sw.clone()) for _ in range(nset)]
+                ms = time_graph(lambda i: (lambda: ck.scaled_mm_mxfp8(*ops_[i])), nset, max(steps // 4, 5),
                                 warmup, check=lambda outs: [same(o, ref) or sys.exit("graph mismatch c4") for o in outs])
+                del ops_
                 res["scaled_mm_mxfp8"] = {"ms": ms, **roofline_flops(FLOPS["scaled_mm_mxfp8"], ms, FP8_PEAK_TFLOPS,
                                                                       traffic.get("scaled_mm_mxfp8"))}
                 log(f"c4 scaled_mm_mxfp8: {ms * 1e3:.1f} us")
@@ -272,8 +289,12 @@ def run_gpu(configs, steps, warmup, log):
         qw, sw = ck.quantize_nvfp4(w, gw)
         try:
             ref = ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)
-            ms = time_graph(lambda i: (lambda: ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)), 2, max(steps // 4, 5),
-                            warmup, check=lambda outs: [same(o, ref) or sys.exit("graph mismatch c5 mm") for o in outs])
+            nset = _sets_for(qa.numel() + qw.numel())
+            ops_ = [(qa.clone(), qw.clone(), sa.clone(), sw.clone()) for _ in range(nset)]
+            ms = time_graph(lambda i: (lambda: ck.scaled_mm_nvfp4(ops_[i][0], ops_[i][1], ga, gw, ops_[i][2], ops_[i][3])),
+                            nset, max(steps // 4, 5), warmup,
+                            check=lambda outs: [same(o, ref) or sys.exit("graph mismatch c5 mm") for o in outs])
+            del ops_
             r = roofline_flops(FLOPS["scaled_mm_nvfp4"], ms, BF16_PEAK_TFLOPS, traffic.get("scaled_mm_nvfp4"))
             r["frac_of_fp4_peak"] = round(r["achieved"] / FP4_PEAK_TFLOPS, 4)
             res["scaled_mm_nvfp4"] = {"ms": ms, **r}
@@ -288,15 +309,16 @@ def run_cpu_baseline(configs, log):
     """Time the CPU oracle (restatement of the reference eager path) on bounded samples."""
     from oracle import eager_ref as ref
 
-    cores = os.cpu_count() or 1
-    torch.set_num_threads(cores)
+    # the host share of a one-GPU box is OMP_NUM_THREADS cores, not os.cpu_count()
+    torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1))
+    cores = torch.get_num_threads()
     out = {}
     if "c3" in configs:
         x = make_c3()
-        s, reps = time_cpu(lambda: ref.quantize_mxfp8(x))
+        s, reps = time_cpu(lambda: ref.quantize_mxfp8(x), budget_s=12.0)
         out["quantize_mxfp8"] = {"value": round(BYTES["quantize_mxfp8"] / s / 1e9, 3), "unit": "GB/s",
                                  "cores": cores, "kind": "port",
-                                 "sample": f"full C3 tensor [4608, 3072] bf16, median of {reps} runs"}
+                                 "sample": f"full C3 tensor [4608, 3072] bf16, median of {reps} runs (~12 s of CPU work)"}
         log(f"cpu quantize_mxfp8: {s * 1e3:.1f} ms")
     if "c1" in configs:
         x, scale = make_c1()
@@ -321,11 +343,118 @@ def run_cpu_baseline(configs, log):
         x = make_c3()[:512]
         wq, ws = ref.quantize_mxfp8(make_c4_weight())
         xq, xs = ref.quantize_mxfp8(x)
-        s, reps = time_cpu(lambda: ref.scaled_mm_mxfp8_ref(xq, wq, xs, ws), min_reps=1, budget_s=10)
+        s, reps = time_cpu(lambda: ref.scaled_mm_mxfp8_ref(xq, wq, xs, ws), min_reps=1, budget_s=5.0)
         out["scaled_mm_mxfp8"] = {"value": round(2 * 512 * 12288 * 3072 / s / 1e12, 4), "unit": "TFLOP/s",
                                   "cores": cores, "kind": "port",
                                   "sample": f"512 of 4608 rows of A: dequantize + fp32 matmul, median of {reps}"}
     return out
+
+
+# ------------------------------------------------------------------ PMC traffic
+# `--pmc-driver` makes the dispatch sequence that two rocprofv3 --pmc passes count
+# (FETCH_SIZE, then WRITE_SIZE); `--summarize-pmc` turns them into HBM bytes per launch
+# in profiles/traffic.json, which the roofline lines report as `traffic`.
+PMC_CALLS = 3
+PMC_CALIB_BYTES = 256 << 20
+
+
+def pmc_sequence(configs, dev):
+    """(op name, zero-arg launcher) in the order `--pmc-driver` dispatches them."""
+    import comfy_kitchen as ck
+
+    seq = []
+    if "c1" in configs:
+        x, scale = make_c1(dev)
+        q = ck.quantize_per_tensor_fp8(x, scale)
+        seq += [("quantize_per_tensor_fp8", lambda: ck.quantize_per_tensor_fp8(x, scale)),
+                ("dequantize_per_tensor_fp8", lambda: ck.dequantize_per_tensor_fp8(q, scale))]
+    if "c2" in configs:
+        qq, kk, f = make_c2(dev)
+        seq += [("apply_rope", lambda: ck.apply_rope(qq, kk, f)), ("apply_rope1", lambda: ck.apply_rope1(qq, f))]
+    if "c3" in configs or "c4" in configs:
+        x3 = make_c3(dev)
+        qa, sa = ck.quantize_mxfp8(x3)
+        if "c3" in configs:
+            seq.append(("quantize_mxfp8", lambda: ck.quantize_mxfp8(x3)))
+        if "c4" in configs:
+            qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
+            seq.append(("scaled_mm_mxfp8", lambda: ck.scaled_mm_mxfp8(qa, qw, sa, sw)))
+    if "c5" in configs:
+        a, w, ga, gw = make_c5(dev)
+        na, nsa = ck.quantize_nvfp4(a, ga)
+        nw, nsw = ck.quantize_nvfp4(w, gw)
+        seq += [("quantize_nvfp4", lambda: ck.quantize_nvfp4(a, ga)),
+                ("scaled_mm_nvfp4", lambda: ck.scaled_mm_nvfp4(na, nw, ga, gw, nsa, nsw))]
+    return seq
+
+
+def pmc_driver(configs):
+    """One calibration kernel (negate 256 MiB of fp32: reads and writes PMC_CALIB_BYTES), then
+    PMC_CALLS eager calls of each op; no hipMemset/copy between them."""
+    dev = torch.device("cuda", 0)
+    seq = pmc_sequence(configs, dev)
+    src = torch.ones(PMC_CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    torch.neg(src, out=dst)
+    for _, fn in seq:
+        for _ in range(PMC_CALLS):
+            fn()
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_sequence": [n for n, _ in seq], "calls": PMC_CALLS}), flush=True)
+
+
+def _pmc_dispatches(d: Path, counter: str):
+    """[(dispatch id, kernel name, value)] of one counter from a rocprofv3 --pmc csv directory."""
+    import csv
+
+    rows = []
+    for f in sorted(d.rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return rows
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str, configs, command: str):
+    """HBM bytes per launch of each op: counter KiB scaled by calibration bytes / calibration KiB."""
+    seq = [n for n, _ in pmc_sequence_names(configs)]
+    out = {"bytes_per_launch": {}, "calibration": {}, "command": command}
+    for key, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        rows = _pmc_dispatches(Path(d), counter)
+        n = len(seq) * PMC_CALLS
+        ours = [i for i, r in enumerate(rows) if "ckh::" in r[1]]  # the ops' own kernels
+        ops = [rows[i] for i in ours[-n:]]
+        # calibration: the largest non-ckh dispatch just before the measured sequence
+        calib = max((r for r in rows[max(0, ours[-n] - 3):ours[-n]] if "ckh::" not in r[1]), key=lambda r: r[2])
+        factor = PMC_CALIB_BYTES / (calib[2] * 1024.0)
+        out["calibration"][counter] = {"kernel": calib[1][:60], "kib": calib[2], "factor": round(factor, 4)}
+        for i, name in enumerate(seq):
+            vals = [v for _, _, v in ops[i * PMC_CALLS:(i + 1) * PMC_CALLS]]
+            b = sum(vals) / len(vals) * 1024.0 * factor
+            out["bytes_per_launch"].setdefault(name, {})[key] = round(b)
+    for name, v in out["bytes_per_launch"].items():
+        v["total"] = v.get("fetch", 0) + v.get("write", 0)
+    (REPO / "profiles").mkdir(exist_ok=True)
+    (REPO / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+
+
+def pmc_sequence_names(configs):
+    names = []
+    if "c1" in configs:
+        names += ["quantize_per_tensor_fp8", "dequantize_per_tensor_fp8"]
+    if "c2" in configs:
+        names += ["apply_rope", "apply_rope1"]
+    if "c3" in configs:
+        names.append("quantize_mxfp8")
+    if "c4" in configs:
+        names.append("scaled_mm_mxfp8")
+    if "c5" in configs:
+        names += ["quantize_nvfp4", "scaled_mm_nvfp4"]
+    return [(n, None) for n in names]
 
 
 def main():
@@ -335,7 +464,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc-driver", action="store_true", help="dispatch sequence for rocprofv3 --pmc passes")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc output directories")
+    ap.add_argument("--pmc-command", default="", help="command recorded in profiles/traffic.json")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc, set(args.configs.split(",")), args.pmc_command)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the quantizers/GEMMs shard by rows with no exchange; see DESIGN.md).", file=sys.stderr)
@@ -351,6 +487,9 @@ def main():
 
     if not ck.list_backends()["hip"]["available"]:
         sys.exit(f"hip backend unavailable: {ck.list_backends()['hip']['unavailable_reason']}")
+    if args.pmc_driver:
+        pmc_driver(configs)
+        return
     gpu = run_gpu(configs, args.steps, args.warmup, log)
     cpu = {} if args.no_cpu else run_cpu_baseline(configs, log)
 
