@@ -108,6 +108,17 @@ def scaled_mm_mxfp8(a: torch.Tensor, b: torch.Tensor, block_scale_a: torch.Tenso
     return torch.ops.comfy_kitchen.scaled_mm_mxfp8(a, b, block_scale_a, block_scale_b, bias, code)
 
 
+def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                  bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """y = scale_a * scale_b * (a @ b.T) + bias on per-tensor E4M3 operands (both K-major).
+
+    Not part of the reference's public API: it is the matmul behind TensorCoreFP8Layout's
+    linear / mm / addmm, where the reference calls torch F.scaled_mm (scaled_mm_v2.py:27-53).
+    """
+    code = DTYPE_TO_CODE[out_dtype if out_dtype is not None else torch.bfloat16]
+    return torch.ops.comfy_kitchen.scaled_mm_fp8(a, b, scale_a, scale_b, bias, code)
+
+
 def apply_rope(xq: torch.Tensor, xk: torch.Tensor,
                freqs_cis: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Rotate query and key by the 2x2 matrices in freqs_cis [..., head_dim/2, 2, 2]."""

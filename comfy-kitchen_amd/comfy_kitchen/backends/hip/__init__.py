@@ -32,6 +32,7 @@ __all__ = [
     "quantize_mxfp8",
     "quantize_nvfp4",
     "quantize_per_tensor_fp8",
+    "scaled_mm_fp8",
     "scaled_mm_mxfp8",
     "scaled_mm_nvfp4",
 ]
@@ -53,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_dequantize_nvfp4": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _u64]),
     "ckh_apply_rope": (_i32, [_p, _p, _p, _p, _p] + [_i64] * 13 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_mxfp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
+    "ckh_scaled_mm_fp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
 }
 ABI_VERSION = 1
@@ -258,6 +260,24 @@ def scaled_mm_mxfp8(a: torch.Tensor, b: torch.Tensor, block_scale_a: torch.Tenso
     return out
 
 
+def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                  bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    out_dtype = out_dtype or torch.bfloat16
+    a, b = a.contiguous(), b.contiguous()
+    m, k = a.shape
+    n, kb = b.shape
+    if k != kb:
+        raise ValueError(f"scaled_mm_fp8: K mismatch {k} vs {kb}")
+    sa = _scalar_on(scale_a, a.device, "scale_a")
+    sb = _scalar_on(scale_b, a.device, "scale_b")
+    bias_t, bias_code = _bias_args(bias, n, a.device)
+    out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    with _on_device(a):
+        _call("ckh_scaled_mm_fp8", a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), _ptr(bias_t),
+              out.data_ptr(), m, n, k, DTYPE_TO_CODE[out_dtype], bias_code, _stream(a))
+    return out
+
+
 def scaled_mm_nvfp4(a: torch.Tensor, b: torch.Tensor, tensor_scale_a: torch.Tensor,
                     tensor_scale_b: torch.Tensor, block_scale_a: torch.Tensor,
                     block_scale_b: torch.Tensor, bias: torch.Tensor | None = None,
@@ -363,6 +383,14 @@ def _build_constraints() -> dict:
                               block_scale_b=ParamConstraint(dtypes=frozenset({torch.float8_e8m0fnu})),
                               bias=ParamConstraint(dtypes=floats),
                               out_dtype=ParamConstraint(dtypes=floats)),
+        "scaled_mm_fp8": fc(a=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
+                                              shape_rules=two_d + (DivisibleBy(1, 16),)),
+                            b=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
+                                              shape_rules=two_d + (DivisibleBy(1, 16),)),
+                            scale_a=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
+                            scale_b=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
+                            bias=ParamConstraint(dtypes=floats),
+                            out_dtype=ParamConstraint(dtypes=floats)),
         "scaled_mm_nvfp4": fc(a=ParamConstraint(dtypes=frozenset({torch.uint8}),
                                                 shape_rules=two_d + (DivisibleBy(1, 16),)),
                               b=ParamConstraint(dtypes=frozenset({torch.uint8}),

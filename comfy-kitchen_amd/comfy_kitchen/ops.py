@@ -140,6 +140,18 @@ def _(a, b, block_scale_a, block_scale_b, bias, output_dtype_code):
     return torch.empty((a.shape[0], b.shape[0]), dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code], device=a.device)
 
 
+@torch.library.custom_op("comfy_kitchen::scaled_mm_fp8", mutates_args=())
+def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
+                  bias: torch.Tensor | None, output_dtype_code: int) -> torch.Tensor:
+    return _dispatch("scaled_mm_fp8", a=a, b=b, scale_a=scale_a, scale_b=scale_b, bias=bias,
+                     out_dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code])
+
+
+@scaled_mm_fp8.register_fake
+def _(a, b, scale_a, scale_b, bias, output_dtype_code):
+    return torch.empty((a.shape[0], b.shape[0]), dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code], device=a.device)
+
+
 # ------------------------------------------------------------------------- RoPE
 @torch.library.custom_op("comfy_kitchen::apply_rope", mutates_args=())
 def apply_rope(xq: torch.Tensor, xk: torch.Tensor, freqs_cis: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -109,6 +109,9 @@ struct Args {
     int ncb;               // scale column blocks: ceil(K/32/4)
     int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
     int tiles_m, tiles_n;
+    // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
+    const float* tsa;
+    const float* tsb;
 };
 
 // Register-staged loads of one operand for a pair of stages (s, s + 1), i.e. K bytes
@@ -279,7 +282,9 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
     else return load1<BIAS>(bias, n);
 }
 
-template <int OUT, int BIAS>
+// UNIT: per-tensor FP8 (TensorCoreFP8Layout): no block scales (every MFMA scale byte is
+// E8M0 127 = 1.0) and out = tsa * tsb * (A B^T) + bias.
+template <int OUT, int BIAS, bool UNIT>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     // Stage buffers 0, 1 and 2, 3 in two arrays.  Every stage reads fragments from one
     // array and writes staged data into the other, so the compiler knows they never
@@ -324,18 +329,23 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     ScaleWords SW;
     auto load_b = [&](int s) {
         load_pair(LB, SB, s * BK, p.K);
-        load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
+        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
     auto store_b = [&](auto x_c, auto y_c) {
         store_pair(LB, SB, buf(x_c), buf(y_c));
-        store_scales(SW, buf(x_c) + 2 * TILE, buf(y_c) + 2 * TILE, wave, lane);
+        if constexpr (!UNIT) store_scales(SW, buf(x_c) + 2 * TILE, buf(y_c) + 2 * TILE, wave, lane);
     };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
     const int hs = 8 * half;
     auto read_scales = [&](auto b_c, uint32_t (&sb)[4], uint32_t (&sa)[4]) {
+        if constexpr (UNIT) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sb[t] = sa[t] = 0x7f7f7f7fu;
+            return;
+        }
         const uint8_t* st = buf(b_c) + 2 * TILE;
         const v4u wb = *reinterpret_cast<const v4u*>(st + wn * 512 + r32 * 16);
         const v4u wa = *reinterpret_cast<const v4u*>(st + STILE + wm * 512 + r32 * 16);
@@ -379,7 +389,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             constexpr int i = k / 4, j = k % 4;
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.b[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
                                                                         OPSEL, sca[j]);
-            if constexpr (k == 0) {
+            if constexpr (k == 0 && !UNIT) {
                 wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + wn * 512 + r32 * 16);
                 wa = *reinterpret_cast<const v4u*>(nx + 2 * TILE + STILE + wm * 512 + r32 * 16);
             }
@@ -396,15 +406,15 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
                     load_piece<k>(LB, SB, add);
                 }
             }
-            if constexpr (k == 8) {
+            if constexpr (k == 8 && !UNIT) {
                 if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
                 else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
             }
             if constexpr (k == 12) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    nb[u] = wb[u] >> hs;
-                    na[u] = wa[u] >> hs;
+                    nb[u] = UNIT ? 0x7f7f7f7fu : wb[u] >> hs;
+                    na[u] = UNIT ? 0x7f7f7f7fu : wa[u] >> hs;
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -446,6 +456,11 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
     // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
     // n = 8*g + 4*half (+0..3) of weight tile i.
+    const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
+    auto value = [&](float a, int n) {
+        if constexpr (UNIT) a *= alpha;
+        return a + (n < p.N ? bias_at<BIAS>(p.bias, n) : 0.0f);
+    };
     if constexpr (OUT != CKH_F32) {
         // 16-bit output: stage the tile in LDS as 256 rows of 512 bytes, the 64-row slab
         // q in buffer q.  The pitch EPI_ROW = 520 spreads the 32 rows of one fragment
@@ -463,8 +478,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
                     const int n = n0 + nl;
                     float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[e] = acc[i][j][4 * g + e] + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
+                    for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * g + e], n + e);
                     uint32_t w0 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[0]) : f_to_f16(v[0])) |
                                   ((OUT == CKH_BF16 ? f_to_bf16_rne(v[1]) : f_to_f16(v[1])) << 16);
                     uint32_t w1 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[2]) : f_to_f16(v[2])) |
@@ -504,8 +518,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
                     const int n = n0 + wn * 128 + i * 32 + 8 * g + 4 * half;
                     float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[e] = acc[i][j][4 * g + e] + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
+                    for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * g + e], n + e);
                     const int64_t idx = static_cast<int64_t>(m) * p.N + n;
                     if (n + 3 < p.N && (p.N & 3) == 0) {
                         store4<OUT>(p.out, idx, v);
@@ -525,6 +538,43 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
 using namespace ckh;
 
+namespace {
+
+template <bool UNIT>
+int launch_gemm(const mx::Args& p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT>), grid, dim3(mx::NT), 0, st, p)
+#define BY_BIAS(O)                                         \
+    do {                                                   \
+        if (!has_bias) LAUNCH(O, -1);                      \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
+        else LAUNCH(O, CKH_BF16);                          \
+    } while (0)
+    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+    else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef LAUNCH
+    return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
+}
+
+mx::Args base_args(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N, int64_t K) {
+    mx::Args p{};
+    p.a = static_cast<const uint8_t*>(a);
+    p.b = static_cast<const uint8_t*>(b);
+    p.bias = bias;
+    p.out = out;
+    p.M = static_cast<int>(M);
+    p.N = static_cast<int>(N);
+    p.K = static_cast<int>(K);
+    p.tiles_m = static_cast<int>(cdiv(M, mx::BM));
+    p.tiles_n = static_cast<int>(cdiv(N, mx::BN));
+    return p;
+}
+
+}  // namespace
+
 extern "C" int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa, const void* sb, const void* bias,
                                    void* out, int64_t M, int64_t N, int64_t K, int out_code, int bias_code,
                                    uintptr_t stream) {
@@ -540,35 +590,32 @@ extern "C" int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa,
     CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sa, 4) && aligned(sb, 4) && aligned(out, 16),
                 "scaled_mm_mxfp8: pointers misaligned");
     if (M == 0 || N == 0) return CKH_OK;
-    mx::Args p{};
-    p.a = static_cast<const uint8_t*>(a);
-    p.b = static_cast<const uint8_t*>(b);
+    mx::Args p = base_args(a, b, bias, out, M, N, K);
     p.sa = static_cast<const uint8_t*>(sa);
     p.sb = static_cast<const uint8_t*>(sb);
-    p.bias = bias;
-    p.out = out;
-    p.M = static_cast<int>(M);
-    p.N = static_cast<int>(N);
-    p.K = static_cast<int>(K);
     p.ncb = static_cast<int>(cdiv(K / 32, 4));
     p.sa_rows = static_cast<int>(rup(M, 128));
     p.sb_rows = static_cast<int>(rup(N, 128));
-    p.tiles_m = static_cast<int>(cdiv(M, mx::BM));
-    p.tiles_n = static_cast<int>(cdiv(N, mx::BN));
-    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B>), grid, dim3(mx::NT), 0, st, p)
-#define BY_BIAS(O)                                         \
-    do {                                                   \
-        if (!bias) LAUNCH(O, -1);                          \
-        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
-        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
-        else LAUNCH(O, CKH_BF16);                          \
-    } while (0)
-    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
-    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
-    else BY_BIAS(CKH_F32);
-#undef BY_BIAS
-#undef LAUNCH
-    return check_launch("scaled_mm_mxfp8");
+    return launch_gemm<false>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const float* scale_b,
+                                 const void* bias, void* out, int64_t M, int64_t N, int64_t K, int out_code,
+                                 int bias_code, uintptr_t stream) {
+    CKH_REQUIRE(a && b && scale_a && scale_b && out, "scaled_mm_fp8: null pointer");
+    CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_fp8: sizes must be M, N >= 0 and K > 0");
+    CKH_REQUIRE(K % 16 == 0, "scaled_mm_fp8: K (%lld) must be a multiple of 16", (long long)K);
+    CKH_REQUIRE(M * K < (1ll << 31) && N * K < (1ll << 31) && K < (1ll << 24),
+                "scaled_mm_fp8: operand larger than 2 GiB");
+    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
+                "scaled_mm_fp8: unsupported output dtype code %d", out_code);
+    CKH_REQUIRE(!bias || bias_code == CKH_F32 || bias_code == CKH_F16 || bias_code == CKH_BF16,
+                "scaled_mm_fp8: unsupported bias dtype code %d", bias_code);
+    CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(scale_a, 4) && aligned(scale_b, 4) && aligned(out, 16),
+                "scaled_mm_fp8: pointers misaligned");
+    if (M == 0 || N == 0) return CKH_OK;
+    mx::Args p = base_args(a, b, bias, out, M, N, K);
+    p.tsa = scale_a;
+    p.tsb = scale_b;
+    return launch_gemm<true>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
 }

@@ -135,13 +135,24 @@ int ckh_apply_rope(const void* xq, const void* xk, const void* freqs, void* xq_o
  * MXFP8 GEMM: out[M,N] = sum_k A[m,k]*2^(sa-127) * B[n,k]*2^(sb-127) (+ bias[n]).
  * a [M,K] e4m3, b [N,K] e4m3 (both K-major), sa/sb E8M0 swizzled with logical shapes
  * [M, K/32] / [N, K/32]; bias NULL or [N] of bias_code (f32/f16/bf16);
- * out [M,N] row-major of out_code (f32/f16/bf16).  K % 128 == 0.
+ * out [M,N] row-major of out_code (f32/f16/bf16).  K % 32 == 0.
  * No native counterpart in the reference (eager quantization.py:367-402 routes to
  * torch F.scaled_mm via scaled_mm_v2.py:27-53); replaces that call.
  */
 int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa, const void* sb,
                         const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                         int out_code, int bias_code, uintptr_t stream);
+
+/*
+ * Per-tensor FP8 GEMM: out[M,N] = scale_a * scale_b * sum_k A[m,k] * B[n,k] (+ bias[n]).
+ * a [M,K] e4m3, b [N,K] e4m3 (both K-major), scale_a / scale_b one f32 each on device;
+ * bias NULL or [N] of bias_code; out [M,N] row-major of out_code.  K % 16 == 0.
+ * Replaces the TensorWise torch F.scaled_mm call behind TensorCoreFP8Layout's
+ * linear / mm / addmm (tensor/fp8.py:86-101 -> scaled_mm_v2.py:27-53).
+ */
+int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const float* scale_b,
+                      const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                      int out_code, int bias_code, uintptr_t stream);
 
 /*
  * NVFP4 GEMM: out[M,N] = alpha * sum_k E2M1(a)*sa[m,k/16] * E2M1(b)*sb[n,k/16] (+bias[n]).
