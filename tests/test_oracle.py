@@ -189,3 +189,116 @@ def test_swap_nibbles_and_hi_first():
     assert torch.equal(ck.swap_nibbles(qh), ql)
     assert torch.equal(sh.view(torch.uint8), sl.view(torch.uint8))
     assert torch.equal(ref.dequantize_nvfp4(qh, g, sh), ref.dequantize_nvfp4(ql, g, sl, hi_first=False))
+
+
+# --------------------------------------------------------------------- RoPE
+def _rotation(theta: torch.Tensor) -> torch.Tensor:
+    """[..., 2, 2] rotation matrices [[cos, -sin], [sin, cos]] (the Flux EmbedND layout)."""
+    c, s = torch.cos(theta), torch.sin(theta)
+    return torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2)
+
+
+def test_rope_identity_and_quarter_turn():
+    """Closed forms: the identity rotation returns x exactly; a quarter turn maps each
+    pair (x0, x1) to (-x1, x0) exactly (every product is by 0 or +-1)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 3, 10, 16, generator=g).bfloat16()
+    ident = _rotation(torch.zeros(1, 1, 10, 8, dtype=torch.float64)).float()
+    assert torch.equal(ref.apply_rope1(x, ident), x)
+    quarter = torch.tensor([[0.0, -1.0], [1.0, 0.0]]).expand(1, 1, 10, 8, 2, 2).contiguous()
+    out = ref.apply_rope1(x, quarter).reshape(1, 3, 10, 8, 2)
+    xp = x.reshape(1, 3, 10, 8, 2)
+    assert torch.equal(out[..., 0], -xp[..., 1]) and torch.equal(out[..., 1], xp[..., 0])
+
+
+def test_rope_matches_complex_rotation_within_one_ulp():
+    """Against a float64 complex multiply (x0 + i x1) * e^{i theta}: the oracle computes in
+    fp32 and rounds once to bf16, so it must sit within 1 bf16 ULP of the exact rotation.
+    A swapped sign or transposed matrix would be off by far more."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 4, 33, 64, generator=g).bfloat16()
+    theta = torch.rand(1, 1, 33, 32, generator=g, dtype=torch.float64) * 6.3
+    got = ref.apply_rope1(x, _rotation(theta).float()).double().reshape(2, 4, 33, 32, 2)
+    z = torch.complex(x.double().reshape(2, 4, 33, 32, 2)[..., 0], x.double().reshape(2, 4, 33, 32, 2)[..., 1])
+    r = z * torch.exp(1j * theta)
+    for comp, exact in ((got[..., 0], r.real), (got[..., 1], r.imag)):
+        ulp = torch.where(exact.abs() > 0, 2.0 ** (torch.floor(torch.log2(exact.abs())) - 7), 2.0 ** -133)
+        assert bool(((comp - exact).abs() <= ulp).all())
+    # apply_rope is apply_rope1 on each of q and k
+    xk = torch.randn(2, 4, 33, 64, generator=g).bfloat16()
+    q2, k2 = ref.apply_rope(x, xk, _rotation(theta).float())
+    assert torch.equal(q2, ref.apply_rope1(x, _rotation(theta).float()))
+    assert torch.equal(k2, ref.apply_rope1(xk, _rotation(theta).float()))
+
+
+# ------------------------------------------------------------ GEMM references
+E2M1_VALUES = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+
+
+def _swz(r, c, n_cb):
+    return (((r // 128) * n_cb + c // 4) * 32 + r % 32) * 16 + ((r % 128) // 32) * 4 + c % 4
+
+
+def test_scaled_mm_mxfp8_ref_bruteforce():
+    """Tiny MXFP8 GEMM summed element by element in float64 from raw code/scale bytes."""
+    g = torch.Generator().manual_seed(8)
+    m, n, k = 3, 2, 64
+    a = torch.randint(0, 256, (m, k), generator=g, dtype=torch.uint8)
+    b = torch.randint(0, 256, (n, k), generator=g, dtype=torch.uint8)
+    a[(a & 0x7F) == 0x7F] = 0x12  # no NaN codes
+    b[(b & 0x7F) == 0x7F] = 0x34
+    sa = torch.zeros(128 * 4, dtype=torch.uint8)
+    sb = torch.zeros(128 * 4, dtype=torch.uint8)
+    ea = torch.randint(120, 134, (m, 2), generator=g)
+    eb = torch.randint(120, 134, (n, 2), generator=g)
+    for r in range(m):
+        for c in range(2):
+            sa[_swz(r, c, 1)] = int(ea[r, c])
+    for r in range(n):
+        for c in range(2):
+            sb[_swz(r, c, 1)] = int(eb[r, c])
+    av = a.view(torch.float8_e4m3fn).double()
+    bv = b.view(torch.float8_e4m3fn).double()
+    y = ref.scaled_mm_mxfp8_ref(a.view(torch.float8_e4m3fn), b.view(torch.float8_e4m3fn),
+                                sa.view(torch.float8_e8m0fnu), sb.view(torch.float8_e8m0fnu), out_dtype=torch.float32)
+    for i in range(m):
+        for j in range(n):
+            s = sum(float(av[i, kk]) * 2.0 ** (int(ea[i, kk // 32]) - 127) * float(bv[j, kk]) *
+                    2.0 ** (int(eb[j, kk // 32]) - 127) for kk in range(k))
+            assert abs(y[i, j].item() - s) <= 1e-5 * max(1.0, abs(s))
+
+
+def test_scaled_mm_nvfp4_ref_bruteforce():
+    """Tiny NVFP4 GEMM from raw nibbles (even element in the high nibble), E4M3 block
+    scales and the two tensor scales, summed in float64."""
+    g = torch.Generator().manual_seed(9)
+    m, n, k = 2, 3, 32
+    qa = torch.randint(0, 256, (m, k // 2), generator=g, dtype=torch.uint8)
+    qb = torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.uint8)
+    ca = torch.randint(0x20, 0x50, (m, 2), generator=g, dtype=torch.uint8)  # normal E4M3 scales
+    cb = torch.randint(0x20, 0x50, (n, 2), generator=g, dtype=torch.uint8)
+    sa = torch.zeros(128 * 4, dtype=torch.uint8)
+    sb = torch.zeros(128 * 4, dtype=torch.uint8)
+    for r in range(m):
+        for c in range(2):
+            sa[_swz(r, c, 1)] = int(ca[r, c])
+    for r in range(n):
+        for c in range(2):
+            sb[_swz(r, c, 1)] = int(cb[r, c])
+    ts_a, ts_b = torch.tensor([0.75]), torch.tensor([1.25])
+
+    def val(q, row, kk):
+        byte = int(q[row, kk // 2])
+        nib = (byte >> 4) if kk % 2 == 0 else (byte & 15)
+        return (-1.0 if nib & 8 else 1.0) * E2M1_VALUES[nib & 7]
+
+    def e4m3(byte):
+        return float(torch.tensor([byte], dtype=torch.uint8).view(torch.float8_e4m3fn).double())
+
+    y = ref.scaled_mm_nvfp4_ref(qa, qb, ts_a, ts_b, sa.view(torch.float8_e4m3fn), sb.view(torch.float8_e4m3fn),
+                                out_dtype=torch.float32)
+    for i in range(m):
+        for j in range(n):
+            s = sum(val(qa, i, kk) * e4m3(int(ca[i, kk // 16])) * val(qb, j, kk) * e4m3(int(cb[j, kk // 16]))
+                    for kk in range(k)) * 0.75 * 1.25
+            assert abs(y[i, j].item() - s) <= 1e-5 * max(1.0, abs(s))
