@@ -6,21 +6,36 @@
 // 16 elements in the 32_4_4 swizzled layout; alpha: one fp32 on the device
 // (tensor_scale_a * tensor_scale_b).
 //
-// Exact fold: E2M1 * E4M3 has at most 5 significant bits and lies in [2^-10, 2688],
-// so every product value * block scale is an exact fp16.  The global -> LDS stage
-// decodes each byte (two E2M1 codes) with v_cvt_scalef32_pk_f16_fp4 and multiplies
-// by the block scale with a packed f16 multiply, and the MFMAs (v_mfma_f32_32x32x16_f16) multiply the
-// exact fp16 operands with fp32 accumulation; alpha and bias are applied in the
-// epilogue.  (An E8M0-scaled FP4 MFMA cannot take E4M3 block scales exactly, and a
-// lossy re-encode misses the 1e-2 accuracy bar.)  Nibble order inside a byte does
-// not matter: both operands use the same packing, and the dot product is invariant
-// under the same permutation of k on both sides.
+// Arithmetic.  The gfx950 block-scaled MFMAs take only power-of-two (E8M0) scales, and
+// E2M1 * E4M3 needs up to 5 significant bits, so no FP8/FP6/FP4 element format holds
+// the scaled values exactly.  Each E2M1 code times its E4M3 block scale is an exact
+// fp16 (magnitudes in [2^-10, 2688]), so the operands are decoded to fp16 in registers
+// (v_cvt_scalef32_pk_f16_fp4 with scale 1, then a packed multiply by the block scale,
+// itself converted with v_cvt_scalef32_pk_f16_fp8) and multiplied with
+// v_mfma_f32_32x32x16_f16 (fp32 accumulation); alpha and bias are applied in the
+// epilogue.  Any consistent assignment of k to MFMA lanes gives the same dot product,
+// so both operands use the same one and nibble order inside a byte does not matter.
 //
-// Tiling matches the MXFP8 kernel: 256 (m) x 256 (n) per 256-thread workgroup, 4 waves
-// of 128 x 128, K advancing 64 elements per stage (32 packed bytes per row) through
-// double-buffered LDS holding fp16 tiles (128 bytes per row per stage), 16-byte chunk
-// c of row r stored at chunk c ^ (r & 7) ^ ((r >> 3) & 1).  MFMA operand layout: lane
-// l = 32*h + r holds row r, k = 16*kk + 8*h .. +7 of the 64-wide stage.
+// Tiling: a 256-thread workgroup computes a 256 (m) x 256 (n) tile, 4 waves of
+// 128 x 128 (4 x 4 MFMA tiles, 256 fp32 accumulators per lane).  A stage is 64 K
+// elements: 32 packed bytes per row and one 32-bit word of four block scales per row.
+// Packed codes and scale words go to LDS unchanged (4x less LDS traffic than fp16
+// tiles) in groups of 4 stages (one 128-byte line per row), double-buffered, by
+// buffer_load_dwordx4 ... lds: 18 direct-to-LDS loads per wave per group, one barrier
+// per group, and a whole group (~8000 MFMA cycles) of latency cover.
+//
+// Within a stage each lane needs, per 32-row tile, 16 bytes (32 codes: k = 32h ..
+// 32h+31 of the stage for lane half h, of which MFMA substep kk uses bytes 4kk..4kk+3)
+// and the tile row's scale word (blocks 2h and 2h+1 are its); one ds_read_b128 each.
+// The decode of substep kk+1 (VALU, independent of the MFMAs in flight) is placed by
+// the compiler's scheduler between the 16 MFMAs of substep kk.
+//
+// LDS rows are 128 bytes (a group); logical 16-byte chunk c of row r is stored at
+// chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.  Workgroups
+// walk the tiles XCD-contiguously as in the MXFP8 kernel.
+#include <type_traits>
+#include <utility>
+
 #include "ckh_common.h"
 
 namespace ckh {
@@ -30,15 +45,39 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int BM = 256, BN = 256, BKE = 64 /* elements */, NT = 256;
-constexpr int ROWB = 128;                 // LDS bytes per row per stage (64 fp16)
-constexpr int TILE_BYTES = 256 * ROWB;
+constexpr int BM = 256, BN = 256, NT = 256;
+constexpr int SKB = 32;                     // packed bytes per row per stage (64 elements)
+constexpr int GS = 4;                       // stages per group
+constexpr int GKB = SKB * GS;               // bytes per row per group: one 128-byte line
+constexpr int TILE = 256 * GKB;             // one operand's codes per group (32 KB)
+constexpr int STILE = 256 * 4 * GS;         // one operand's scale words per group (4 KB)
+constexpr int GBUF = 2 * TILE + 2 * STILE;  // one group buffer: b codes, a codes, b scales, a scales
+constexpr int EPI_ROW = 520;                // bytes of one staged 16-bit output row (512 + 8 pad)
+static_assert(128 * EPI_ROW <= GBUF, "half the output tile must fit one group buffer");
+constexpr int LOADS_PER_GROUP = 18;         // per wave: 8 + 8 code loads, 2 scale loads
 
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * ROWB + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4); }
+// s_waitcnt immediate: vmcnt in [3:0] and [15:14], expcnt [6:4] (left at 7), lgkmcnt 0
+constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | ((vm >> 4) << 14); }
+
+// Barrier after an explicit wait; the empty asm statements keep memory operations from
+// moving across (a __syncthreads() fence would also drain the prefetched group).
+template <int WAITCNT>
+__device__ __forceinline__ void group_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAITCNT);
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+    void* up = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(up, 0, static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
+                                             0x00020000);
 }
 
 struct Args {
@@ -50,60 +89,89 @@ struct Args {
     const void* bias;
     void* out;
     int M, N, K;  // K in elements
-    int ncb;      // scale column blocks: ceil(K/16/4)
+    int ncb;      // scale word columns: ceil(K/16/4)
     int sa_rows, sb_rows;
     int tiles_m, tiles_n;
 };
 
-// Per stage each thread owns (row tid>>1 and row 128 + tid>>1) x (16 packed bytes =
-// 32 elements = 2 scale blocks, half tid&1 of the 64-element stage).
-struct Stage {
-    v4u q[2];        // packed codes
-    uint32_t s[2];   // the row's scale word for this stage
+// Direct-to-LDS loads of one operand's group.  Wave w, load j (0..7) covers rows
+// R = 64 w + 8 j .. +7 (1 KB of LDS); lane i fills row R + i/8, physical chunk i%8,
+// which holds logical chunk (i%8) ^ (i/8) (R is a multiple of 8).
+struct Loader {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t voff;     // lane's byte offset for j = 0 and group 0
+    int cbyte;         // 16 * logical chunk
+    uint32_t rowstep;  // 8 rows
 };
 
-__device__ __forceinline__ void load_stage(__amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rss, int row0, int Kb,
-                                           int k0, int ncb, int tid, Stage& st) {
-    const int hh = tid & 1;
-    const int kb = k0 / 2 + hh * 16;  // packed byte column
-    const uint32_t add = kb < Kb ? static_cast<uint32_t>(kb) : 0x80000000u;
+__device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int Kb, int wave, int lane) {
+    Loader L;
+    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * Kb);
+    const int row = 64 * wave + (lane >> 3);
+    L.cbyte = ((lane & 7) ^ (lane >> 3)) << 4;
+    L.voff = static_cast<uint32_t>(row * Kb + L.cbyte);
+    L.rowstep = 8u * Kb;
+    return L;
+}
+
+__device__ __forceinline__ void issue_codes(const Loader& L, uint8_t* dst, int wave, int kb0, int Kb) {
+    const uint32_t add = (kb0 + L.cbyte < Kb) ? static_cast<uint32_t>(kb0) : 0x80000000u;  // past K: zeros
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = (tid >> 1) + 128 * i;
-        st.q[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<uint32_t>(row) * Kb + add, 0, 0);
-        st.s[i] = __builtin_amdgcn_raw_buffer_load_b32(
-            rss, static_cast<uint32_t>(swz_offset(row0 + row, k0 >> 4, ncb)), 0, 0);
+    for (int j = 0; j < 8; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + (64 * wave + 8 * j) * GKB), 16,
+                                                 L.voff + j * L.rowstep + add, 0, 0, 0);
+}
+
+// Scale words of a group: for a 256-row tile, 128-row block rb and word column c, the
+// 512-byte chunk ((rb0 + rb) * ncb + c) of the swizzled tensor; the 4 columns of a group
+// are contiguous, so each block's group is one 2 KB run.  Wave w copies block rb = w & 1
+// of operand w >> 1 (0 = weight, 1 = activation): 2 loads of 1 KB.  Columns past the
+// last (ncb) and blocks past the padded rows arrive as zeros.  Inside a chunk row r's
+// word sits at (r % 32) * 16 + ((r % 128) / 32) * 4.
+__device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a, int rb0_b,
+                                             int rb0_a, int ncb, int g, uint8_t* sdst, int wave, int lane) {
+    const int op = wave >> 1, rb = wave & 1;
+    const __amdgpu_buffer_rsrc_t rs = op ? rs_a : rs_b;
+    const int base = (op ? rb0_a : rb0_b) + rb;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int col = GS * g + 2 * q + (lane >> 5);
+        const uint32_t off =
+            col < ncb ? static_cast<uint32_t>((base * ncb + col) * 512 + (lane & 31) * 16) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(sdst + op * STILE + rb * 2048 + q * 1024), 16, off,
+                                                 0, 0, 0);
     }
 }
 
-// Decode one thread's 2 x 32 elements to fp16 (exact) and write them to LDS.  The
-// hardware fp4 -> f16 convert applies only a power-of-two scale, so it decodes with
-// scale 1 and the E4M3 block scale (exact in fp16) is applied by a packed f16
-// multiply, which is exact for these products.
-__device__ __forceinline__ void store_stage(uint8_t* __restrict__ lds, int tid, const Stage& st) {
-    const int hh = tid & 1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = (tid >> 1) + 128 * i;
-        // the two E4M3 block scales of this half: bytes 2*hh and 2*hh+1 of the word
-        const _Float16 s0 = static_cast<_Float16>(e4m3_to_f((st.s[i] >> (16 * hh)) & 0xffu));
-        const _Float16 s1 = static_cast<_Float16>(e4m3_to_f((st.s[i] >> (16 * hh + 8)) & 0xffu));
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {  // 16-byte LDS chunk = 8 fp16 = 4 packed bytes
-            const uint32_t w = st.q[i][c];
-            const v2h sc = c < 2 ? v2h{s0, s0} : v2h{s1, s1};
-            v2h h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * sc;
-            v2h h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * sc;
-            v2h h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * sc;
-            v2h h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * sc;
-            v8h v = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-            *reinterpret_cast<v8h*>(lds + lds_off(row, 4 * hh + c)) = v;
-        }
-    }
+// One stage's raw operands for this lane: per tile 16 code bytes + the scale word.
+struct Raw {
+    v4u b[4], a[4];
+    v4u wb, wa;  // scale words of tiles 0..3
+};
+
+// Decoded fp16 operands of one MFMA substep.
+struct Dec {
+    v8h b[4], a[4];
+};
+
+// 4 bytes of E2M1 codes -> 8 fp16, times the block scale pair s (exact).
+__device__ __forceinline__ v8h decode8(uint32_t w, v2h s) {
+    const v2h e0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s;
+    const v2h e1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s;
+    const v2h e2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s;
+    const v2h e3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s;
+    return v8h{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
 }
 
-__device__ __forceinline__ v8h load_frag(const uint8_t* __restrict__ lds, int row, int kk, int half) {
-    return *reinterpret_cast<const v8h*>(lds + lds_off(row, 2 * kk + half));
+// The lane half's two block scales (bytes 2h and 2h+1 of the word) as fp16; sh = 16 h.
+__device__ __forceinline__ v2h scale_pair(uint32_t word, int sh) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word >> sh, 1.0f, false);
+}
+
+template <int OUT>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+    return (OUT == CKH_BF16 ? f_to_bf16_rne(x) : f_to_f16(x)) |
+           ((OUT == CKH_BF16 ? f_to_bf16_rne(y) : f_to_f16(y)) << 16);
 }
 
 template <int OUT>
@@ -111,18 +179,15 @@ __device__ __forceinline__ void store4(void* out, int64_t idx, const float (&v)[
     if constexpr (OUT == CKH_F32) {
         *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
-        uint32_t w0 = (OUT == CKH_BF16 ? f_to_bf16(v[0]) : f_to_f16(v[0])) |
-                      ((OUT == CKH_BF16 ? f_to_bf16(v[1]) : f_to_f16(v[1])) << 16);
-        uint32_t w1 = (OUT == CKH_BF16 ? f_to_bf16(v[2]) : f_to_f16(v[2])) |
-                      ((OUT == CKH_BF16 ? f_to_bf16(v[3]) : f_to_f16(v[3])) << 16);
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + idx) = make_uint2(w0, w1);
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + idx) =
+            make_uint2(pack2<OUT>(v[0], v[1]), pack2<OUT>(v[2], v[3]));
     }
 }
 
 template <int OUT>
 __device__ __forceinline__ void store1(void* out, int64_t idx, float v) {
     if constexpr (OUT == CKH_F32) static_cast<float*>(out)[idx] = v;
-    else static_cast<uint16_t*>(out)[idx] = static_cast<uint16_t>(OUT == CKH_BF16 ? f_to_bf16(v) : f_to_f16(v));
+    else static_cast<uint16_t*>(out)[idx] = static_cast<uint16_t>(OUT == CKH_BF16 ? f_to_bf16_rne(v) : f_to_f16(v));
 }
 
 template <int BIAS>
@@ -133,7 +198,8 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 
 template <int OUT, int BIAS>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[4 * TILE_BYTES];  // [2 stages][weight, act][tile]
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
 
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -142,17 +208,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave & 1, wn = wave >> 1;
     const int half = lane >> 5, r32 = lane & 31;
     const int Kb = p.K / 2;
 
-    const __amdgpu_buffer_rsrc_t rsb = make_rsrc(p.b + static_cast<int64_t>(n0) * Kb,
-                                                static_cast<uint32_t>(min(BN, p.N - n0)) * Kb);
-    const __amdgpu_buffer_rsrc_t rsa = make_rsrc(p.a + static_cast<int64_t>(m0) * Kb,
-                                                static_cast<uint32_t>(min(BM, p.M - m0)) * Kb);
+    const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * Kb, min(BN, p.N - n0), Kb, wave, lane);
+    const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * Kb, min(BM, p.M - m0), Kb, wave, lane);
     const __amdgpu_buffer_rsrc_t rssb = make_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = make_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
+    const int NG = (Kb + GKB - 1) / GKB;  // groups of 256 elements
 
     v16f acc[4][4];
 #pragma unroll
@@ -160,64 +226,174 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
 
-    const int KT = (p.K + BKE - 1) / BKE;
-    Stage sb, sa;
-    load_stage(rsb, rssb, n0, Kb, 0, p.ncb, tid, sb);
-    load_stage(rsa, rssa, m0, Kb, 0, p.ncb, tid, sa);
-    store_stage(smem, tid, sb);
-    store_stage(smem + TILE_BYTES, tid, sa);
+    auto gbuf = [&](auto g_c) -> uint8_t* { return (decltype(g_c)::value & 1) ? lds1 : lds0; };
+    auto issue_group = [&](auto g_c, int g) {
+        uint8_t* d = gbuf(g_c);
+        issue_codes(LB, d, wave, g * GKB, Kb);
+        issue_codes(LA, d + TILE, wave, g * GKB, Kb);
+        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, g, d + 2 * TILE, wave, lane);
+    };
+
+    // lane's fragment and scale-word addresses inside a group buffer
+    const int x7 = r32 & 7;
+    const uint32_t frow_b = static_cast<uint32_t>((wn * 128 + r32) * GKB);
+    const uint32_t frow_a = static_cast<uint32_t>(TILE + (wm * 128 + r32) * GKB);
+    const uint32_t sw_b = static_cast<uint32_t>(2 * TILE + wn * 2048 + r32 * 16);
+    const uint32_t sw_a = static_cast<uint32_t>(2 * TILE + STILE + wm * 2048 + r32 * 16);
+    auto read_raw = [&](const uint8_t* gb, auto s_c, Raw& R) {
+        constexpr int S = decltype(s_c)::value;
+        const uint32_t chunk = static_cast<uint32_t>(((2 * S + half) ^ x7) << 4);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            R.b[t] = *reinterpret_cast<const v4u*>(gb + frow_b + t * 32 * GKB + chunk);
+            R.a[t] = *reinterpret_cast<const v4u*>(gb + frow_a + t * 32 * GKB + chunk);
+        }
+        R.wb = *reinterpret_cast<const v4u*>(gb + sw_b + S * 512);
+        R.wa = *reinterpret_cast<const v4u*>(gb + sw_a + S * 512);
+    };
+    const int sh = 16 * half;
+    // decode substep kk of R into D: dword kk of each tile, block 2h + kk/2
+    auto decode = [&](const Raw& R, auto kk_c, Dec& D) {
+        constexpr int KK = decltype(kk_c)::value;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const v2h pb = scale_pair(R.wb[t], sh);
+            const v2h pa = scale_pair(R.wa[t], sh);
+            const v2h sbt = KK < 2 ? v2h{pb[0], pb[0]} : v2h{pb[1], pb[1]};
+            const v2h sat = KK < 2 ? v2h{pa[0], pa[0]} : v2h{pa[1], pa[1]};
+            D.b[t] = decode8(R.b[t][KK], sbt);
+            D.a[t] = decode8(R.a[t][KK], sat);
+        }
+    };
+    auto mfma16 = [&](const Dec& D) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(D.b[i], D.a[j], acc[i][j], 0, 0, 0);
+    };
+    Raw R0, R1;
+    Dec D0, D1;
+    using G0 = std::integral_constant<int, 0>;
+    using G1 = std::integral_constant<int, 1>;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    using K0 = std::integral_constant<int, 0>;
+    using K1 = std::integral_constant<int, 1>;
+    using K2 = std::integral_constant<int, 2>;
+    using K3 = std::integral_constant<int, 3>;
+
+    // One stage: the MFMAs of substeps 0..3 on R (each substep decoded one ahead), the
+    // next stage's raw operands read into Rn during substep 1, and substep 0 of Rn
+    // decoded during substep 3.  Before the last stage of a group reads the next group,
+    // that group must be resident: wait for this wave's loads, barrier (after which no
+    // wave reads group g's buffer any more), then refill that buffer with group g + 2.
+    auto stage = [&](auto g_c, auto s_c, int g, Raw& R, Raw& Rn) {
+        constexpr int G = decltype(g_c)::value, S = decltype(s_c)::value;
+        using GN = std::integral_constant<int, (S == GS - 1) ? (G ^ 1) : G>;
+        using SN = std::integral_constant<int, (S + 1) % GS>;
+        if constexpr (S == GS - 1) {
+            group_barrier<waitcnt_vm_lgkm0(0)>();
+            issue_group(g_c, g + 2);
+        }
+        decode(R, K1{}, D1);
+        mfma16(D0);
+        read_raw(gbuf(GN{}), SN{}, Rn);
+        decode(R, K2{}, D0);
+        mfma16(D1);
+        decode(R, K3{}, D1);
+        mfma16(D0);
+        decode(Rn, K0{}, D0);
+        mfma16(D1);
+    };
+
+    // prologue: groups 0 and 1 in flight, group 0 resident, stage 0 read and decoded
+    issue_group(G0{}, 0);
+    issue_group(G1{}, 1);
+    group_barrier<waitcnt_vm_lgkm0(LOADS_PER_GROUP)>();
+    read_raw(lds0, S0{}, R0);
+    decode(R0, K0{}, D0);
+
+    // groups in pairs (buffer = group % 2); groups past K are all zeros
+    for (int g = 0; g < NG; g += 2) {
+        stage(G0{}, S0{}, g, R0, R1);
+        stage(G0{}, S1{}, g, R1, R0);
+        stage(G0{}, S2{}, g, R0, R1);
+        stage(G0{}, S3{}, g, R1, R0);
+        stage(G1{}, S0{}, g + 1, R0, R1);
+        stage(G1{}, S1{}, g + 1, R1, R0);
+        stage(G1{}, S2{}, g + 1, R0, R1);
+        stage(G1{}, S3{}, g + 1, R1, R0);
+    }
+    // the loads of the groups past the end still write LDS, which the epilogue reuses
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < KT;
-        if (more) {
-            load_stage(rsb, rssb, n0, Kb, (kt + 1) * BKE, p.ncb, tid, sb);
-            load_stage(rsa, rssa, m0, Kb, (kt + 1) * BKE, p.ncb, tid, sa);
-        }
-        const uint8_t* lb = smem + cur * 2 * TILE_BYTES;
-        const uint8_t* la = lb + TILE_BYTES;
+    // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
+    // n = 8*gg + 4*half (+0..3) of weight tile i; times alpha, plus bias.
+    const float alpha = p.alpha[0];
+    auto value = [&](float a, int n) { return a * alpha + (n < p.N ? bias_at<BIAS>(p.bias, n) : 0.0f); };
+    if constexpr (OUT != CKH_F32) {
+        // Stage the 16-bit tile in LDS as 256 rows of EPI_ROW bytes (rows 0..127 in
+        // buffer 0, 128..255 in buffer 1; the 520-byte pitch spreads a fragment's 32 rows
+        // over distinct bank pairs), then each wave stores 64 whole rows, 64 lanes x 8 bytes.
+        auto row_ptr = [&](int r) -> uint8_t* { return r < 128 ? lds0 + r * EPI_ROW : lds1 + (r - 128) * EPI_ROW; };
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            v8h fa[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) fa[t] = load_frag(la, wm * 128 + t * 32 + r32, kk, half);
+        for (int j = 0; j < 4; ++j) {
+            uint8_t* rowp = row_ptr(wm * 128 + j * 32 + r32);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const v8h fb = load_frag(lb, wn * 128 + i * 32 + r32, kk, half);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb, fa[j], acc[i][j], 0, 0, 0);
+                for (int gg = 0; gg < 4; ++gg) {
+                    const int nl = wn * 128 + i * 32 + 8 * gg + 4 * half;
+                    const int n = n0 + nl;
+                    *reinterpret_cast<uint2*>(rowp + nl * 2) =
+                        make_uint2(pack2<OUT>(value(acc[i][j][4 * gg], n), value(acc[i][j][4 * gg + 1], n + 1)),
+                                   pack2<OUT>(value(acc[i][j][4 * gg + 2], n + 2), value(acc[i][j][4 * gg + 3], n + 3)));
+                }
             }
         }
-        if (more) {
-            uint8_t* nb = smem + (cur ^ 1) * 2 * TILE_BYTES;
-            store_stage(nb, tid, sb);
-            store_stage(nb + TILE_BYTES, tid, sa);
-        }
         __syncthreads();
-    }
-
-    const float alpha = p.alpha[0];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + r32;
-        if (m >= p.M) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int n = n0 + wn * 128 + i * 32 + 8 * g + 4 * half;
-                float v[4];
+        const int n = n0 + 4 * lane;
+        const bool vec = (p.N & 3) == 0 && n + 4 <= p.N;
+        const int rows = min(64, p.M - (m0 + wave * 64));
+        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64) * p.N + n;
+#pragma unroll 8
+        for (int rl = 0; rl < 64; ++rl) {
+            const uint2 d = *reinterpret_cast<const uint2*>(row_ptr(wave * 64 + rl) + lane * 8);
+            if (rl >= rows) break;
+            uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
+            if (vec) {
+                *reinterpret_cast<uint2*>(o) = d;
+            } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    v[e] = acc[i][j][4 * g + e] * alpha + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
-                const int64_t idx = static_cast<int64_t>(m) * p.N + n;
-                if (n + 3 < p.N && (p.N & 3) == 0) {
-                    store4<OUT>(p.out, idx, v);
-                } else {
+                    if (n + e < p.N) o[e] = static_cast<uint16_t>((e < 2 ? d.x : d.y) >> (16 * (e & 1)));
+            }
+        }
+    } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < p.N) store1<OUT>(p.out, idx + e, v[e]);
+        for (int j = 0; j < 4; ++j) {
+            const int m = m0 + wm * 128 + j * 32 + r32;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    const int n = n0 + wn * 128 + i * 32 + 8 * gg + 4 * half;
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * gg + e], n + e);
+                    const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+                    if (n + 3 < p.N && (p.N & 3) == 0) {
+                        store4<OUT>(p.out, idx, v);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) store1<OUT>(p.out, idx + e, v[e]);
+                    }
                 }
             }
         }
@@ -241,7 +417,7 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
                 "scaled_mm_nvfp4: unsupported output dtype code %d", out_code);
     CKH_REQUIRE(!bias || bias_code == CKH_F32 || bias_code == CKH_F16 || bias_code == CKH_BF16,
                 "scaled_mm_nvfp4: unsupported bias dtype code %d", bias_code);
-    CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sa, 4) && aligned(sb, 4) && aligned(out, 16) &&
+    CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sa, 16) && aligned(sb, 16) && aligned(out, 16) &&
                     aligned(alpha, 4),
                 "scaled_mm_nvfp4: pointers misaligned");
     if (M == 0 || N == 0) return CKH_OK;
@@ -264,12 +440,12 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_kernel<O, B>), grid, dim3(nv::NT), 0, st, p)
-#define BY_BIAS(O)                                          \
-    do {                                                    \
-        if (!bias) LAUNCH(O, -1);                           \
-        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32);  \
-        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16);  \
-        else LAUNCH(O, CKH_BF16);                           \
+#define BY_BIAS(O)                                         \
+    do {                                                   \
+        if (!bias) LAUNCH(O, -1);                          \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
+        else LAUNCH(O, CKH_BF16);                          \
     } while (0)
     if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
     else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
