@@ -84,6 +84,41 @@ __device__ __forceinline__ uint32_t f_to_bf16_rne(float f) {
     return hb;
 }
 
+// ------------------------------------------------- hardware convert helpers
+// gfx950's convert instructions, each checked against the software encoders above on
+// all 2^32 fp32 inputs (after the callers' clamps): v_cvt_pk_fp8_f32 == f_to_e4m3,
+// v_cvt_pk_bf8_f32 == f_to_e5m2 and v_cvt_scalef32_pk_fp4_f32 (scale 1) == f_to_e2m1
+// for every non-NaN input in range, v_cvt_pk_bf16_f32 == f_to_bf16 for every non-NaN
+// input, and v_cvt_f32_fp8 == e4m3_to_f for every code.  A NaN input gives some NaN
+// code whose sign / payload may differ from the software's, so callers that must keep
+// the software's NaN bytes take a software path when a NaN is present.
+
+// four E4M3 / E5M2 codes (byte i = code of x_i), inputs already clamped to the range
+__device__ __forceinline__ uint32_t hw_e4m3x4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true));
+}
+__device__ __forceinline__ uint32_t hw_e5m2x4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true));
+}
+
+// E4M3 code in byte B of w -> float (exact)
+template <int B>
+__device__ __forceinline__ float hw_e4m3_to_f(uint32_t w) {
+    return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(w), B);
+}
+
+__device__ __forceinline__ bool is_nan(float f) { return (as_u(f) & 0x7fffffffu) > 0x7f800000u; }
+
+// Round to the precision of dtype code C through the hardware converts (NaN -> some NaN).
+template <int C>
+__device__ __forceinline__ float round_to_hw(float f) {
+    if constexpr (C == CKH_BF16) return bf16_to_f(f_to_bf16_rne(f));
+    else if constexpr (C == CKH_F16) return round_f16(f);
+    else return f;
+}
+
 // Round a float to the precision of dtype code `c` (f32 is the identity).
 template <int C>
 __device__ __forceinline__ float round_to(float f) {

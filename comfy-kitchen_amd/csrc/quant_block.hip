@@ -53,7 +53,14 @@ __device__ __forceinline__ uint32_t absmax_bits(const float (&v)[8]) {
 // e = 0 and the only other subnormals, 2^-127 < s < 2^-126, give e = 1.  Non-finite
 // amax gives e = 0, as the reference's float->int32 conversion of ceil(log2(inf/NaN))
 // does on x86.
+//
+// For amax with a biased exponent >= 10 the division folds away: amax/448 =
+// (1.f / 1.75) * 2^(E-8) with 1.f the significand, so s is a power of two only when
+// 1.f == 1.75 exactly, and e = E - 8 + (f > 0.75).  (Checked against the division form
+// on all 2^31 non-negative floats.)
 __device__ __forceinline__ uint32_t mx_exponent(uint32_t amax_bits) {
+    if (amax_bits >= (10u << 23) && amax_bits < 0x7f800000u)
+        return (amax_bits >> 23) - 8u + ((amax_bits & 0x7fffffu) > 0x600000u);
     if (amax_bits == 0 || amax_bits >= 0x7f800000u) return 0;
     uint32_t s = as_u(as_f(amax_bits) / 448.0f);
     if (s <= 0x00400000u) return 0;
@@ -77,15 +84,14 @@ __device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_b
         return make_uint2(w[0], w[1]);
     }
     // x / 2^(e-127) == x * 2^(127-e) exactly (both correctly rounded); 1 <= e <= 254
-    // keeps 2^(127-e) a normal float.
+    // keeps 2^(127-e) a normal float.  Here amax is finite and 2^(e-127) >= amax/448, so
+    // every |q| <= 448: the reference's clamp is a no-op and the hardware convert
+    // (RNE, identical to f_to_e4m3 on this range) encodes directly.
     const float mul = as_f((254u - e) << 23);
+    float q[8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        float q = v[t] * mul;
-        q = q > 448.0f ? 448.0f : (q < -448.0f ? -448.0f : q);
-        w[t >> 2] |= f_to_e4m3(q) << (8 * (t & 3));
-    }
-    return make_uint2(w[0], w[1]);
+    for (int t = 0; t < 8; ++t) q[t] = v[t] * mul;
+    return make_uint2(hw_e4m3x4(q[0], q[1], q[2], q[3]), hw_e4m3x4(q[4], q[5], q[6], q[7]));
 }
 
 template <int IN>
@@ -122,14 +128,13 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __
 // Per 16-element block (reference eager quantization.py:137-158):
 //   s8 = E4M3(min(amax/6/g, 448)); T = g*s8; codes = E2M1(clamp(x/T, +-6)), T==0 -> +0.
 // Divisions are IEEE fp32 divisions, as in the reference's eager path.
-template <int IN>
+template <int IN, bool HI_FIRST>
 __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __restrict__ x,
                                                                   const float* __restrict__ gptr,
                                                                   uint8_t* __restrict__ qx,
                                                                   uint32_t* __restrict__ sc, int64_t rows,
                                                                   int64_t cols, int64_t orows, int64_t ocols,
-                                                                  int64_t n_cb, int64_t n_units, bool vec_ok,
-                                                                  bool hi_first) {
+                                                                  int64_t n_cb, int64_t n_units, bool vec_ok) {
     const int64_t unit = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 3;
     if (unit >= n_units) return;  // whole 8-lane units leave together
     const int l = threadIdx.x & 7;
@@ -147,27 +152,42 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 
     float c = (as_f(m) / 6.0f) / g;
     c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
-    const uint32_t s8 = live ? f_to_e4m3(c) : 0u;
+    // c >= 0 and <= 448 unless NaN: the hardware E4M3 convert is exact there
+    const uint32_t s8 = !live ? 0u : is_nan(c) ? f_to_e4m3(c) : (hw_e4m3x4(c, 0.0f, 0.0f, 0.0f) & 0xffu);
     const float T = g * e4m3_to_f(s8);
 
     if (live) {
-        uint32_t codes[8];
-        if (T == 0.0f) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) codes[t] = 0;
-        } else {
+        uint32_t w = 0;
+        if (T != 0.0f) {
+            float q[8];
+            bool any_nan = false;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                float q = v[t] / T;
-                q = q > 6.0f ? 6.0f : (q < -6.0f ? -6.0f : q);
-                codes[t] = f_to_e2m1(q);
+                q[t] = __builtin_amdgcn_fmed3f(v[t] / T, -6.0f, 6.0f);
+                any_nan |= is_nan(v[t] / T);
             }
-        }
-        uint32_t w = 0;
+            if (!any_nan) {
+                // hardware E2M1 pairs: the first operand lands in the low nibble
+                const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of the pair for the low nibble
+                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[0 + f], q[0 + o], 1.0f, 0);
+                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[2 + f], q[2 + o], 1.0f, 1);
+                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[4 + f], q[4 + o], 1.0f, 2);
+                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[6 + f], q[6 + o], 1.0f, 3);
+            } else {  // software codes keep the reference's NaN behaviour
+                uint32_t codes[8];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            uint32_t b = hi_first ? ((codes[2 * p] << 4) | codes[2 * p + 1]) : ((codes[2 * p + 1] << 4) | codes[2 * p]);
-            w |= b << (8 * p);
+                for (int t = 0; t < 8; ++t) {
+                    float qq = v[t] / T;
+                    qq = qq > 6.0f ? 6.0f : (qq < -6.0f ? -6.0f : qq);
+                    codes[t] = f_to_e2m1(qq);
+                }
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t b = HI_FIRST ? ((codes[2 * p] << 4) | codes[2 * p + 1])
+                                          : ((codes[2 * p + 1] << 4) | codes[2 * p]);
+                    w |= b << (8 * p);
+                }
+            }
         }
         *reinterpret_cast<uint32_t*>(qx + r * (cols / 2) + k0 / 2) = w;
     }
@@ -298,12 +318,18 @@ extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void*
     uint8_t* q = static_cast<uint8_t*>(qx);
     uint32_t* s = static_cast<uint32_t*>(scales);
     const bool hf = hi_first != 0;
-#define LAUNCH(I)                                                                                              \
-    hipLaunchKernelGGL((quantize_nvfp4_kernel<I>), grid, dim3(kThreads), 0, st, x, g, q, s, rows, cols, \
-                       orig_rows, orig_cols, n_cb, n_units, vec_ok, hf)
-    if (in_code == CKH_F32) LAUNCH(CKH_F32);
-    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
-    else LAUNCH(CKH_BF16);
+#define LAUNCH(I, H)                                                                                \
+    hipLaunchKernelGGL((quantize_nvfp4_kernel<I, H>), grid, dim3(kThreads), 0, st, x, g, q, s, rows, cols, \
+                       orig_rows, orig_cols, n_cb, n_units, vec_ok)
+#define BY_ORDER(I)          \
+    do {                     \
+        if (hf) LAUNCH(I, true); \
+        else LAUNCH(I, false);   \
+    } while (0)
+    if (in_code == CKH_F32) BY_ORDER(CKH_F32);
+    else if (in_code == CKH_F16) BY_ORDER(CKH_F16);
+    else BY_ORDER(CKH_BF16);
+#undef BY_ORDER
 #undef LAUNCH
     return check_launch("quantize_nvfp4");
 }

@@ -40,13 +40,31 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
         float v[16];
         load8<IN>(static_cast<const char*>(x) + i0 * ES, *reinterpret_cast<float(*)[8]>(&v[0]));
         load8<IN>(static_cast<const char*>(x) + (i0 + 8) * ES, *reinterpret_cast<float(*)[8]>(&v[8]));
+        // hardware path: product rounded to x's dtype, clamped, converted in pairs
+        float t[16];
+        bool any_nan = false;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            t[e] = round_to_hw<IN>(v[e] * r);
+            any_nan |= is_nan(t[e]);
+        }
+        constexpr float MX = OUT == CKH_E4M3 ? 448.0f : 57344.0f;
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            uint32_t acc = 0;
+            float c[4];
 #pragma unroll
-            for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
-            w[q] = acc;
+            for (int b = 0; b < 4; ++b) c[b] = __builtin_amdgcn_fmed3f(t[4 * q + b], -MX, MX);
+            w[q] = OUT == CKH_E4M3 ? hw_e4m3x4(c[0], c[1], c[2], c[3]) : hw_e5m2x4(c[0], c[1], c[2], c[3]);
+        }
+        if (any_nan) {  // keep the software's NaN bytes
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t acc = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
+                w[q] = acc;
+            }
         }
         *reinterpret_cast<uint4*>(out + i0) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
@@ -65,6 +83,28 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
     if constexpr (OUT == CKH_F32) reinterpret_cast<float*>(out)[i] = v;
     else if constexpr (OUT == CKH_BF16) reinterpret_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(f_to_bf16(v));
     else reinterpret_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(f_to_f16(v));
+}
+
+// Store 16 rounded outputs starting at element i (16-byte aligned), 16-bit outputs
+// rounded by the hardware converts (callers route NaN-containing data elsewhere).
+template <int OUT>
+__device__ __forceinline__ void store16_hw(void* out, int64_t i, const float (&v)[16]) {
+    if constexpr (OUT == CKH_F32) {
+        float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else {
+        uint32_t w[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * q]) : f_to_f16(v[2 * q]);
+            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
+            w[q] = lo | (hi << 16);
+        }
+        uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i);
+        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
 }
 
 // Store 16 rounded outputs starting at element i (16-byte aligned).
@@ -97,10 +137,29 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
     if (VEC && i0 + kPerThread <= n) {
         uint4 c = *reinterpret_cast<const uint4*>(x + i0);
         uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-        float v[16];
+        // a NaN code (0x7f / 0xff in E4M3) takes the software path, which fixes its bytes
+        bool nan_code = false;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = decode_fp8<IN>((cw[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
-        store16<OUT>(out, i0, v);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t m = cw[q] & 0x7f7f7f7fu;
+            if constexpr (IN == CKH_E4M3) nan_code |= ((m + 0x01010101u) & 0x80808080u) != 0;  // some byte == 0x7f
+            else nan_code = true;
+        }
+        float v[16];
+        if (!nan_code) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[4 * q] = hw_e4m3_to_f<0>(cw[q]) * s;
+                v[4 * q + 1] = hw_e4m3_to_f<1>(cw[q]) * s;
+                v[4 * q + 2] = hw_e4m3_to_f<2>(cw[q]) * s;
+                v[4 * q + 3] = hw_e4m3_to_f<3>(cw[q]) * s;
+            }
+            store16_hw<OUT>(out, i0, v);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = decode_fp8<IN>((cw[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
+            store16<OUT>(out, i0, v);
+        }
     } else {
         for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
     }
