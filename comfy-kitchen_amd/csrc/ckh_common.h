@@ -189,8 +189,16 @@ __device__ __forceinline__ uint32_t e2m1_mag(float a) {
     return (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) +
            (a > 5.0f);
 }
+// A NaN takes the reference's normal-range branch (float_utils.py:96-147 has no NaN
+// case): the magnitude bits are rebiased, rounded to one mantissa bit and truncated to
+// 8 bits, which gives code 2, 3 or 4 for the NaN magnitudes.
 __device__ __forceinline__ uint32_t f_to_e2m1(float v) {
-    return ((as_u(v) >> 28) & 8u) | e2m1_mag(fabsf(v));
+    const uint32_t sign = (as_u(v) >> 28) & 8u;
+    if (is_nan(v)) {
+        const uint32_t m = as_u(v) & 0x7fffffffu;
+        return sign | (((m + (static_cast<uint32_t>(1 - 127) << 23) + (1u << 21) - 1u + ((m >> 22) & 1u)) >> 22) & 0xffu);
+    }
+    return sign | e2m1_mag(fabsf(v));
 }
 // Code -> value (sign in bit 3).
 __device__ __forceinline__ float e2m1_to_f(uint32_t c) {
@@ -210,17 +218,25 @@ __host__ __device__ __forceinline__ int64_t swz_offset(int64_t r, int64_t c, int
 }
 
 // ---------------------------------------------------------- element loads
+// Streaming (nontemporal) 16-byte loads: input read once by a kernel is not kept in the
+// caches.  On gfx950 this lifts the quantizers' bandwidth by 10-15% over plain loads at
+// the benchmark sizes; nontemporal stores measured no better than plain stores.
+typedef unsigned ckh_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+    ckh_u32x4 a = __builtin_nontemporal_load(static_cast<const ckh_u32x4*>(p));
+    return make_uint4(a.x, a.y, a.z, a.w);
+}
+
 // Load 8 consecutive elements of dtype code C as floats from an address aligned to
-// 8 * sizeof(element).
+// 8 * sizeof(element), as a streaming read.
 template <int C>
 __device__ __forceinline__ void load8(const void* p, float (&v)[8]) {
     if constexpr (C == CKH_F32) {
-        const float4* q = reinterpret_cast<const float4*>(p);
-        float4 a = q[0], b = q[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        uint4 a = ld_stream16(p), b = ld_stream16(static_cast<const char*>(p) + 16);
+        v[0] = as_f(a.x); v[1] = as_f(a.y); v[2] = as_f(a.z); v[3] = as_f(a.w);
+        v[4] = as_f(b.x); v[5] = as_f(b.y); v[6] = as_f(b.z); v[7] = as_f(b.w);
     } else {
-        uint4 w = *reinterpret_cast<const uint4*>(p);
+        uint4 w = ld_stream16(p);
         uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

@@ -124,10 +124,203 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __
     if (l == 0) sc[swz_offset(r, 4 * j, n_cb) >> 2] = word;
 }
 
+// ------------------------------------------------------- MXFP8, 16-bit fast path
+// For bf16/f16 inputs with no column padding (orig shape == padded shape up to the
+// 128-row scale padding), cols % 128 == 0, 16-byte aligned, < 2^31 elements.
+//
+// Same units as above, with every step on packed 16-bit data:
+//   * amax: |x| as 16-bit integers, two per register (v_pk_max_u16), then a DPP
+//     quad_perm max over the 4 lanes of a block;
+//   * codes: v_cvt_scalef32_pk_fp8_{bf16,f16} with scale 2^(e-127) computes
+//     E4M3(x / 2^(e-127)) with RNE; it uses the exponent of the scale only and matches
+//     the software encoder on every 16-bit input whose quotient lies in [-448, 448]
+//     (checked for all 2^16 patterns and every normal power-of-two scale), which is
+//     always the case here because 2^(e-127) >= amax/448;
+//   * the scale word is OR-combined with two DPP row_ror steps.
+// Blocks whose amax is zero, tiny (biased exponent < 10) or non-finite take the
+// general encoder.  Row = unit / n_cb by an exact multiply-shift (Granlund-Montgomery:
+// m = ceil(2^(31+l) / n_cb), l = ceil(log2 n_cb), exact for unit < 2^31).
+typedef unsigned short ckh_u16x2 __attribute__((ext_vector_type(2)));
+typedef short ckh_i16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ckh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 ckh_f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t amax16x8(uint4 w) {
+    auto h = [](uint32_t v) { return __builtin_bit_cast(ckh_u16x2, v & 0x7fff7fffu); };
+    ckh_u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(h(w.x), h(w.y)),
+                                            __builtin_elementwise_max(h(w.z), h(w.w)));
+    return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y));
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
+// 16-bit amax bits -> fp32 bits of the same value
+template <int IN>
+__device__ __forceinline__ uint32_t amax16_to_f32_bits(uint32_t m) {
+    if constexpr (IN == CKH_BF16) return m << 16;
+    else return as_u(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(m))));
+}
+
+// Codes of the two packed pairs a, b: E4M3(x / 2^(e-127)), scale = 2^(e-127).
+template <int IN>
+__device__ __forceinline__ uint32_t scaled_e4m3x4(uint32_t a, uint32_t b, float scale) {
+    ckh_i16x2 o = {0, 0};
+    if constexpr (IN == CKH_BF16) {
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, a), scale, false);
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, b), scale, true);
+    } else {
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, a), scale, false);
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, b), scale, true);
+    }
+    return __builtin_bit_cast(uint32_t, o);
+}
+
+template <int IN>
+__device__ __forceinline__ void unpack16x8(uint4 w, float (&v)[8]) {
+    const uint32_t p[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (IN == CKH_BF16) {
+            v[2 * i] = as_f(p[i] << 16);
+            v[2 * i + 1] = as_f(p[i] & 0xffff0000u);
+        } else {
+            ckh_f16x2 h = __builtin_bit_cast(ckh_f16x2, p[i]);
+            v[2 * i] = static_cast<float>(h.x);
+            v[2 * i + 1] = static_cast<float>(h.y);
+        }
+    }
+}
+
+constexpr int kMxUnits = 2;  // units per thread (1, 2 and 4 measured; 2 is fastest)
+
+template <int IN>
+__global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uint16_t* __restrict__ x,
+                                                                       uint8_t* __restrict__ qx,
+                                                                       uint32_t* __restrict__ sc, uint32_t rows,
+                                                                       uint32_t cols, uint32_t n_cb,
+                                                                       uint32_t n_units, uint32_t magic,
+                                                                       uint32_t shift) {
+    const uint32_t l = threadIdx.x & 15;
+    uint4 w[kMxUnits];
+    uint32_t r[kMxUnits], off[kMxUnits], unit[kMxUnits];
+#pragma unroll
+    for (int u = 0; u < kMxUnits; ++u) {
+        unit[u] = (blockIdx.x * kMxUnits + u) * (kThreads / 16) + (threadIdx.x >> 4);
+        r[u] = static_cast<uint32_t>((static_cast<uint64_t>(unit[u]) * magic) >> shift);
+        off[u] = r[u] * cols + 128 * (unit[u] - r[u] * n_cb) + 8 * l;
+        w[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (r[u] < rows) w[u] = ld_stream16(x + off[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kMxUnits; ++u) {
+        uint32_t m = amax16x8(w[u]);
+        m = max(m, dpp<0xB1>(m));  // quad_perm [1,0,3,2]
+        m = max(m, dpp<0x4E>(m));  // quad_perm [2,3,0,1]
+        const uint32_t bits = amax16_to_f32_bits<IN>(m);
+        uint32_t e;
+        uint2 codes;
+        if (bits >= (10u << 23) && bits < 0x7f800000u) {
+            e = (bits >> 23) - 8u + ((bits & 0x7fffffu) > 0x600000u);
+            const float scale = as_f(e << 23);
+            codes = make_uint2(scaled_e4m3x4<IN>(w[u].x, w[u].y, scale), scaled_e4m3x4<IN>(w[u].z, w[u].w, scale));
+        } else {
+            e = mx_exponent(bits);
+            float v[8];
+            unpack16x8<IN>(w[u], v);
+            codes = mx_encode8(v, bits, e);
+        }
+        if (r[u] < rows) *reinterpret_cast<uint2*>(qx + off[u]) = codes;
+        uint32_t word = e << (8 * (l >> 2));
+        word |= dpp<0x124>(word);  // row_ror:4
+        word |= dpp<0x128>(word);  // row_ror:8
+        if (l == 0 && unit[u] < n_units) {
+            const uint32_t j = unit[u] - r[u] * n_cb;
+            sc[(((r[u] >> 7) * n_cb + j) * 32 + (r[u] & 31)) * 4 + ((r[u] & 127) >> 5)] = word;
+        }
+    }
+}
+
 // ------------------------------------------------------------------- NVFP4
 // Per 16-element block (reference eager quantization.py:137-158):
 //   s8 = E4M3(min(amax/6/g, 448)); T = g*s8; codes = E2M1(clamp(x/T, +-6)), T==0 -> +0.
 // Divisions are IEEE fp32 divisions, as in the reference's eager path.
+
+// Pack 8 values already clamped to [-6, 6] into E2M1 nibbles with the hardware convert
+// (RNE, identical to f_to_e2m1 on that range); the convert puts its first operand in
+// the low nibble.
+template <bool HI_FIRST>
+__device__ __forceinline__ uint32_t pack_e2m1x8(const float* q) {
+    const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of each pair that goes to the low nibble
+    uint32_t w = 0;
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[0 + f], q[0 + o], 1.0f, 0);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[2 + f], q[2 + o], 1.0f, 1);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[4 + f], q[4 + o], 1.0f, 2);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[6 + f], q[6 + o], 1.0f, 3);
+    return w;
+}
+
+// NaN blocks: E2M1 has no NaN code, so the reference's codes for NaN data depend on the
+// NaN's bits as its CPU arithmetic (x86 SSE) propagates them: a NaN operand is returned
+// quieted (the first one if both are NaN) and an invalid operation without NaN operands
+// (inf*0, inf/inf) returns the default NaN 0xFFC00000; torch converts the E4M3 NaN
+// codes to 0x7FF00000 | sign.  The functions below reproduce those bits.
+__device__ __forceinline__ float x86_nan(float r, float a, float b) {
+    if (!is_nan(r)) return r;
+    if (is_nan(a)) return as_f(as_u(a) | 0x00400000u);
+    if (is_nan(b)) return as_f(as_u(b) | 0x00400000u);
+    return as_f(0xffc00000u);
+}
+
+// T = g * float(s8) with the reference's NaN bits
+__device__ __forceinline__ float nvfp4_total(float g, uint32_t s8) {
+    const float s = (s8 & 0x7fu) == 0x7fu ? as_f(0x7ff00000u | ((s8 & 0x80u) << 24)) : e4m3_to_f(s8);
+    return x86_nan(g * s, g, s);
+}
+
+// Codes of 8 values for a block with T != 0, by IEEE division (any T, any input).
+template <bool HI_FIRST>
+__device__ __forceinline__ uint32_t nvfp4_codes8_div(const float* v, float T) {
+    float q[8];
+    bool any_nan = false;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        q[t] = __builtin_amdgcn_fmed3f(v[t] / T, -6.0f, 6.0f);
+        any_nan |= is_nan(v[t] / T);
+    }
+    if (!any_nan) return pack_e2m1x8<HI_FIRST>(q);
+    // software codes keep the reference's NaN behaviour
+    uint32_t codes[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        float qq = x86_nan(v[t] / T, v[t], T);
+        qq = qq > 6.0f ? 6.0f : (qq < -6.0f ? -6.0f : qq);  // fp32 clamp returns a NaN unchanged
+        codes[t] = f_to_e2m1(qq);
+    }
+    uint32_t w = 0;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t b = HI_FIRST ? ((codes[2 * p] << 4) | codes[2 * p + 1]) : ((codes[2 * p + 1] << 4) | codes[2 * p]);
+        w |= b << (8 * p);
+    }
+    return w;
+}
+
+// Block scale code s8 from the block amax and the global scale (IEEE divisions).
+// A NaN c keeps the sign the reference's fp32 ops give it: the amax (a |x|) NaN is
+// positive and x86 division returns its first NaN operand, so NaN amax -> 0x7F, and
+// otherwise a NaN g passes its sign; fp32 clamp(max=448) returns the NaN unchanged.
+__device__ __forceinline__ uint32_t nvfp4_scale_code(float amax, float g) {
+    float c = (amax / 6.0f) / g;
+    c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
+    if (is_nan(c)) return is_nan(amax) || !is_nan(g) ? 0x7fu : (0x7fu | ((as_u(g) >> 24) & 0x80u));
+    // 0 <= c <= 448 here (c < 0 only for g < 0, and clamp keeps it): the hardware
+    // E4M3 convert is exact on [-448, 448]
+    return hw_e4m3x4(c, 0.0f, 0.0f, 0.0f) & 0xffu;
+}
+
 template <int IN, bool HI_FIRST>
 __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __restrict__ x,
                                                                   const float* __restrict__ gptr,
@@ -150,52 +343,90 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
     uint32_t m = absmax_bits(v);
     m = max(m, shfl_xor(m, 1));
 
-    float c = (as_f(m) / 6.0f) / g;
-    c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
-    // c >= 0 and <= 448 unless NaN: the hardware E4M3 convert is exact there
-    const uint32_t s8 = !live ? 0u : is_nan(c) ? f_to_e4m3(c) : (hw_e4m3x4(c, 0.0f, 0.0f, 0.0f) & 0xffu);
-    const float T = g * e4m3_to_f(s8);
-
-    if (live) {
-        uint32_t w = 0;
-        if (T != 0.0f) {
-            float q[8];
-            bool any_nan = false;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                q[t] = __builtin_amdgcn_fmed3f(v[t] / T, -6.0f, 6.0f);
-                any_nan |= is_nan(v[t] / T);
-            }
-            if (!any_nan) {
-                // hardware E2M1 pairs: the first operand lands in the low nibble
-                const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of the pair for the low nibble
-                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[0 + f], q[0 + o], 1.0f, 0);
-                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[2 + f], q[2 + o], 1.0f, 1);
-                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[4 + f], q[4 + o], 1.0f, 2);
-                w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[6 + f], q[6 + o], 1.0f, 3);
-            } else {  // software codes keep the reference's NaN behaviour
-                uint32_t codes[8];
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    float qq = v[t] / T;
-                    qq = qq > 6.0f ? 6.0f : (qq < -6.0f ? -6.0f : qq);
-                    codes[t] = f_to_e2m1(qq);
-                }
-#pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    uint32_t b = HI_FIRST ? ((codes[2 * p] << 4) | codes[2 * p + 1])
-                                          : ((codes[2 * p + 1] << 4) | codes[2 * p]);
-                    w |= b << (8 * p);
-                }
-            }
-        }
-        *reinterpret_cast<uint32_t*>(qx + r * (cols / 2) + k0 / 2) = w;
-    }
+    const uint32_t s8 = live ? nvfp4_scale_code(as_f(m), g) : 0u;
+    const float T = nvfp4_total(g, s8);
+    if (live) *reinterpret_cast<uint32_t*>(qx + r * (cols / 2) + k0 / 2) = T != 0.0f ? nvfp4_codes8_div<HI_FIRST>(v, T) : 0u;
 
     uint32_t word = s8 << (8 * (l >> 1));
     word |= shfl_xor(word, 2);
     word |= shfl_xor(word, 4);
     if (l == 0) sc[swz_offset(r, 4 * j, n_cb) >> 2] = word;
+}
+
+// ------------------------------------------------------- NVFP4, 16-bit fast path
+// For bf16/f16 inputs with no column padding, cols % 64 == 0, 16-byte aligned, < 2^31
+// elements.  One lane per 16-element block (two 16-byte streaming loads), four lanes
+// per unit (one scale word), two units per thread.  Per block, s8 and T are computed as
+// above; then y = RN(1/T) by one IEEE division and every element's quotient by one
+// Markstein correction step,
+//   q0 = v*y;  r = fma(-T, q0, v);  q = fma(r, y, q0) with the sign of v,
+// instead of an IEEE division per element.  The E2M1 code of clamp(q, +-6) equals that
+// of clamp(v/T, +-6) for every bf16 and every f16 v and every T: checked exhaustively
+// for all 2^23 significands of T in [1, 2) against all v in [2^-5, 2^5) (both signs),
+// which covers every code boundary; smaller |v| give code 0 and larger |v| code 7 on
+// both sides, and every step scales exactly by powers of two while T lies in
+// [2^-120, 2^120].  (v*y alone gets 516 bf16 and 3904 f16 codes wrong in that domain.)
+// Blocks whose amax is not finite or whose T lies outside that range, and every block
+// when g is not a positive normal float, use the IEEE division per element.
+constexpr int kNvUnits = 2;  // units per thread
+
+template <int IN, bool HI_FIRST>
+__global__ __launch_bounds__(kThreads) void quantize_nvfp4_fast_kernel(const uint16_t* __restrict__ x,
+                                                                       const float* __restrict__ gptr,
+                                                                       uint8_t* __restrict__ qx,
+                                                                       uint32_t* __restrict__ sc, uint32_t rows,
+                                                                       uint32_t cols, uint32_t n_cb,
+                                                                       uint32_t n_units, uint32_t magic,
+                                                                       uint32_t shift) {
+    const uint32_t l = threadIdx.x & 3;
+    const float g = gptr[0];
+    const bool g_ok = g >= 0x1p-126f && g < __builtin_inff();  // false for NaN
+    uint4 w[kNvUnits][2];
+    uint32_t r[kNvUnits], off[kNvUnits], unit[kNvUnits];
+#pragma unroll
+    for (int u = 0; u < kNvUnits; ++u) {
+        unit[u] = (blockIdx.x * kNvUnits + u) * (kThreads / 4) + (threadIdx.x >> 2);
+        r[u] = static_cast<uint32_t>((static_cast<uint64_t>(unit[u]) * magic) >> shift);
+        off[u] = r[u] * cols + 64 * (unit[u] - r[u] * n_cb) + 16 * l;
+        w[u][0] = w[u][1] = make_uint4(0u, 0u, 0u, 0u);
+        if (r[u] < rows) {
+            w[u][0] = ld_stream16(x + off[u]);
+            w[u][1] = ld_stream16(x + off[u] + 8);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kNvUnits; ++u) {
+        const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
+        const uint32_t s8 = r[u] < rows ? nvfp4_scale_code(amax, g) : 0u;
+        const float T = nvfp4_total(g, s8);
+        float v[16];
+        unpack16x8<IN>(w[u][0], *reinterpret_cast<float(*)[8]>(&v[0]));
+        unpack16x8<IN>(w[u][1], *reinterpret_cast<float(*)[8]>(&v[8]));
+        uint2 codes = make_uint2(0u, 0u);
+        if (T != 0.0f) {
+            if (g_ok && amax < __builtin_inff() && T >= 0x1p-120f && T <= 0x1p120f) {
+                const float y = 1.0f / T;
+                float q[16];
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const float q0 = v[t] * y;
+                    const float e = __builtin_fmaf(-T, q0, v[t]);
+                    q[t] = __builtin_amdgcn_fmed3f(__builtin_copysignf(__builtin_fmaf(e, y, q0), v[t]), -6.0f, 6.0f);
+                }
+                codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+            } else {
+                codes = make_uint2(nvfp4_codes8_div<HI_FIRST>(&v[0], T), nvfp4_codes8_div<HI_FIRST>(&v[8], T));
+            }
+        }
+        if (r[u] < rows) *reinterpret_cast<uint2*>(qx + off[u] / 2) = codes;
+        uint32_t word = s8 << (8 * l);
+        word |= dpp<0xB1>(word);  // quad_perm [1,0,3,2]
+        word |= dpp<0x4E>(word);  // quad_perm [2,3,0,1]
+        if (l == 0 && unit[u] < n_units) {
+            const uint32_t j = unit[u] - r[u] * n_cb;
+            sc[(((r[u] >> 7) * n_cb + j) * 32 + (r[u] & 31)) * 4 + ((r[u] & 127) >> 5)] = word;
+        }
+    }
 }
 
 // -------------------------------------------------------------- dequantize
@@ -269,6 +500,15 @@ __global__ __launch_bounds__(kThreads) void dequantize_nvfp4_kernel(const uint8_
 
 using namespace ckh;
 
+// Multiply-shift for unit / d with 0 <= unit < 2^31 (Granlund-Montgomery):
+// l = ceil(log2 d), magic = ceil(2^(31+l) / d) < 2^32, unit / d = (unit * magic) >> (31+l).
+static void magic_div(int64_t d, uint32_t& magic, uint32_t& shift) {
+    uint32_t lg = 0;
+    while ((int64_t(1) << lg) < d) ++lg;
+    magic = static_cast<uint32_t>(((uint64_t(1) << (31 + lg)) + d - 1) / d);
+    shift = 31 + lg;
+}
+
 extern "C" int ckh_quantize_mxfp8(const void* x, void* qx, void* scales, int64_t rows, int64_t cols,
                                   int64_t orig_rows, int64_t orig_cols, int in_code, uintptr_t stream) {
     CKH_REQUIRE(x && qx && scales, "quantize_mxfp8: null pointer");
@@ -283,11 +523,27 @@ extern "C" int ckh_quantize_mxfp8(const void* x, void* qx, void* scales, int64_t
     const int64_t n_cb = cdiv(cols / 32, 4);
     const int64_t n_units = rup(rows, 128) * n_cb;
     const bool vec_ok = aligned(x, 16) && orig_cols % 8 == 0;
-    dim3 grid(static_cast<unsigned>(cdiv(n_units * 16, kThreads)));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint8_t* q = static_cast<uint8_t*>(qx);
     uint32_t* s = static_cast<uint32_t*>(scales);
-#define LAUNCH(I)                                                                                                   \
+    if ((in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 128 == 0 &&
+        aligned(x, 16) && rows * cols < (int64_t(1) << 31) && n_units * 16 + 4 * kThreads * kMxUnits < (int64_t(1) << 31)) {
+        uint32_t magic, shift;
+        magic_div(n_cb, magic, shift);
+        dim3 fgrid(static_cast<unsigned>(cdiv(n_units * 16, kThreads * kMxUnits)));
+        const uint16_t* xx = static_cast<const uint16_t*>(x);
+        const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
+                   n32 = static_cast<uint32_t>(n_cb), u32 = static_cast<uint32_t>(n_units);
+        if (in_code == CKH_BF16)
+            hipLaunchKernelGGL((quantize_mxfp8_fast_kernel<CKH_BF16>), fgrid, dim3(kThreads), 0, st, xx, q, s, r32,
+                               c32, n32, u32, magic, shift);
+        else
+            hipLaunchKernelGGL((quantize_mxfp8_fast_kernel<CKH_F16>), fgrid, dim3(kThreads), 0, st, xx, q, s, r32,
+                               c32, n32, u32, magic, shift);
+        return check_launch("quantize_mxfp8");
+    }
+    dim3 grid(static_cast<unsigned>(cdiv(n_units * 16, kThreads)));
+#define LAUNCH(I)                                                                                                 \
     hipLaunchKernelGGL((quantize_mxfp8_kernel<I>), grid, dim3(kThreads), 0, st, x, q, s, rows, cols, orig_rows, \
                        orig_cols, n_cb, n_units, vec_ok)
     if (in_code == CKH_F32) LAUNCH(CKH_F32);
@@ -312,12 +568,34 @@ extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void*
     const int64_t n_cb = cdiv(cols / 16, 4);
     const int64_t n_units = rup(rows, 128) * n_cb;
     const bool vec_ok = aligned(x, 16) && orig_cols % 8 == 0;
-    dim3 grid(static_cast<unsigned>(cdiv(n_units * 8, kThreads)));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float* g = static_cast<const float*>(global_scale);
     uint8_t* q = static_cast<uint8_t*>(qx);
     uint32_t* s = static_cast<uint32_t*>(scales);
     const bool hf = hi_first != 0;
+    if ((in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 64 == 0 &&
+        aligned(x, 16) && aligned(qx, 8) && rows * cols < (int64_t(1) << 31) &&
+        n_units * 4 + 4 * kThreads * kNvUnits < (int64_t(1) << 31)) {
+        uint32_t magic, shift;
+        magic_div(n_cb, magic, shift);
+        dim3 fgrid(static_cast<unsigned>(cdiv(n_units * 4, kThreads * kNvUnits)));
+        const uint16_t* xx = static_cast<const uint16_t*>(x);
+        const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
+                   n32 = static_cast<uint32_t>(n_cb), u32 = static_cast<uint32_t>(n_units);
+#define LAUNCH_FAST(I, H)                                                                                          \
+    hipLaunchKernelGGL((quantize_nvfp4_fast_kernel<I, H>), fgrid, dim3(kThreads), 0, st, xx, g, q, s, r32, c32, n32, \
+                       u32, magic, shift)
+        if (in_code == CKH_BF16) {
+            if (hf) LAUNCH_FAST(CKH_BF16, true);
+            else LAUNCH_FAST(CKH_BF16, false);
+        } else {
+            if (hf) LAUNCH_FAST(CKH_F16, true);
+            else LAUNCH_FAST(CKH_F16, false);
+        }
+#undef LAUNCH_FAST
+        return check_launch("quantize_nvfp4");
+    }
+    dim3 grid(static_cast<unsigned>(cdiv(n_units * 8, kThreads)));
 #define LAUNCH(I, H)                                                                                \
     hipLaunchKernelGGL((quantize_nvfp4_kernel<I, H>), grid, dim3(kThreads), 0, st, x, g, q, s, rows, cols, \
                        orig_rows, orig_cols, n_cb, n_units, vec_ok)

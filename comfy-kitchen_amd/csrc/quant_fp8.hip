@@ -135,7 +135,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
     const float s = round_to<OUT>(scale[0]);
     const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kPerThread;
     if (VEC && i0 + kPerThread <= n) {
-        uint4 c = *reinterpret_cast<const uint4*>(x + i0);
+        uint4 c = ld_stream16(x + i0);
         uint32_t cw[4] = {c.x, c.y, c.z, c.w};
         // a NaN code (0x7f / 0xff in E4M3) takes the software path, which fixes its bytes
         bool nan_code = false;

@@ -133,12 +133,13 @@ def _check_mx(x, pad):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (96, 32), (130, 4128)])
+@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (96, 32), (130, 4128), (130, 256), (1, 128),
+                                 (257, 640)])
 def test_quantize_mxfp8(dtype, m, k, hip, seed):
     x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1) * 2)).to(dtype)
     x[0, :32] = 0  # zero block
-    x[1, :31] = 0
-    x[1, 31] = -3.0
+    x[-1, :31] = 0
+    x[-1, 31] = -3.0
     _check_mx(x, pad=False)
 
 
@@ -146,6 +147,27 @@ def test_quantize_mxfp8(dtype, m, k, hip, seed):
 def test_quantize_mxfp8_padded(m, k, hip, seed):
     x = (torch.randn(m, k) * 10).bfloat16()
     _check_mx(x, pad=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantize_mxfp8_special_blocks(dtype, hip, seed):
+    # 16-bit inputs with cols % 128 == 0 take the packed fast path; blocks with a zero,
+    # tiny, infinite or NaN amax must leave it for the general encoder.
+    m, k = 200, 384
+    x = torch.randn(m, k) * torch.exp(torch.randn(m, 1) * 6)
+    x[2, :32] = 0.0
+    x[3, 32:64] = -0.0
+    x[4, :32] = 1e-39  # subnormal in f32/bf16, zero in f16
+    x[5, 64:96] = float("inf")
+    x[6, 96:128] = float("-inf")
+    x[7, 7] = float("nan")
+    x[8, 40] = float("inf")
+    x[9, :32] = 2.0 ** -120
+    x[10, 128:160] = 65504.0
+    x[11, 200] = float("nan")
+    x[11, 201] = -1.0
+    x = x.to(dtype)
+    _check_mx(x, pad=False)
 
 
 def test_quantize_mxfp8_config3_full(hip):
@@ -176,12 +198,45 @@ def _check_nv(x, g, pad, hi_first=True):
 
 @pytest.mark.parametrize("hi_first", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (16, 64)])
+@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (16, 64), (130, 192), (1, 64), (257, 320)])
 def test_quantize_nvfp4(dtype, m, k, hi_first, hip, seed):
     x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1))).to(dtype)
     x[0, :16] = 0
     g = (x.float().abs().amax() / 2688).reshape(1)
     _check_nv(x, g, pad=False, hi_first=hi_first)
+
+
+@pytest.mark.parametrize("hi_first", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantize_nvfp4_special_blocks(dtype, hi_first, hip, seed):
+    # 16-bit inputs with cols % 64 == 0 take the fast path (one reciprocal per block and
+    # a Markstein step per element); blocks with a zero, infinite or NaN amax, and
+    # values exactly on E2M1 rounding boundaries, must match the IEEE-division codes.
+    m, k = 200, 256
+    x = torch.randn(m, k) * torch.exp(torch.randn(m, 1) * 4)
+    x[2, :16] = 0.0
+    x[3, 16:32] = -0.0
+    x[4, 0] = float("nan")
+    x[5, 40] = float("inf")
+    x[6, 48:64] = float("-inf")
+    x[7, :16] = 1e-30
+    # one block whose amax gives T = g * 6 exactly: every boundary multiple of T/6
+    x[8, :16] = torch.tensor([6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5.0, 0.5])
+    x = x.to(dtype)
+    finite = x.float().abs().nan_to_num(0.0, 0.0, 0.0)
+    g = (finite.amax() / 2688).reshape(1)
+    _check_nv(x, g, pad=False, hi_first=hi_first)
+
+
+@pytest.mark.parametrize("g", [1.0, 1e-30, 1e-40, 0.0, -0.01, 1e20, 3.0e-3])
+def test_quantize_nvfp4_global_scale_edges(g, hip, seed):
+    # global scales outside the fast path's range (zero, subnormal, negative, huge) take
+    # the IEEE-division path inside the same kernel
+    x = torch.randn(130, 128) * torch.exp(torch.randn(130, 1) * 3)
+    # with g = 1 this block has T = 1 exactly, so its values sit on the E2M1 rounding
+    # boundaries (ties go to the even code)
+    x[1, :16] = torch.tensor([6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5.0, 0.5])
+    _check_nv(x.bfloat16(), torch.tensor([g], dtype=torch.float32), pad=False)
 
 
 @pytest.mark.parametrize("m,k", [(129, 128), (33, 65), (100, 100), (1, 1)])
