@@ -138,8 +138,7 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __
 //     always the case here because 2^(e-127) >= amax/448;
 //   * the scale word is OR-combined with two DPP row_ror steps.
 // Blocks whose amax is zero, tiny (biased exponent < 10) or non-finite take the
-// general encoder.  Row = unit / n_cb by an exact multiply-shift (Granlund-Montgomery:
-// m = ceil(2^(31+l) / n_cb), l = ceil(log2 n_cb), exact for unit < 2^31).
+// general encoder.
 typedef unsigned short ckh_u16x2 __attribute__((ext_vector_type(2)));
 typedef short ckh_i16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 ckh_bf16x2 __attribute__((ext_vector_type(2)));
@@ -194,23 +193,51 @@ __device__ __forceinline__ void unpack16x8(uint4 w, float (&v)[8]) {
     }
 }
 
-constexpr int kMxUnits = 2;  // units per thread (1, 2 and 4 measured; 2 is fastest)
+// Work mapping of the fast kernels.  The swizzled scale words of the units in one
+// 128-row tile and one unit column j form a contiguous 512-byte span, but neighbouring
+// words belong to rows 32 apart, so units processed in row-major order leave every
+// scale line partially written by workgroups on different XCDs (each with its own L2),
+// which costs about as much HBM traffic as a full line per word.  Instead a work item
+// is one 128-row tile x G unit columns (G = 4 for NVFP4, whose 32-byte code runs need
+// 4 units per 128-byte line; 1 for MXFP8), processed by 4 workgroups of 32 rows each
+// that run on the same XCD: workgroups are dispatched round-robin over the 8 XCDs
+// (XCD = blockIdx % 8), so item i gets workgroups 32*(i/8) + i%8 + 8q, q = 0..3, and
+// every scale and code line of the item is written within one XCD.
+struct FastItem {
+    uint32_t tile, q, cg;  // 128-row tile, 32-row group in it, unit-column group
+    bool valid;
+};
+__device__ __forceinline__ FastItem fast_item(uint32_t n_items, uint32_t n_cg, uint32_t cg_magic, uint32_t cg_shift) {
+    const uint32_t b = blockIdx.x, k = b >> 3;
+    const uint32_t item = (k >> 2) * 8 + (b & 7);
+    FastItem f;
+    f.q = k & 3;
+    f.tile = static_cast<uint32_t>((static_cast<uint64_t>(item) * cg_magic) >> cg_shift);
+    f.cg = item - f.tile * n_cg;
+    f.valid = item < n_items;
+    return f;
+}
+
+constexpr int kMxUnits = 2;  // units per thread: 2 passes of 16 units cover a workgroup's 32 rows
 
 template <int IN>
 __global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uint16_t* __restrict__ x,
                                                                        uint8_t* __restrict__ qx,
                                                                        uint32_t* __restrict__ sc, uint32_t rows,
                                                                        uint32_t cols, uint32_t n_cb,
-                                                                       uint32_t n_units, uint32_t magic,
-                                                                       uint32_t shift) {
+                                                                       uint32_t n_items, uint32_t cg_magic,
+                                                                       uint32_t cg_shift) {
+    // item: 128 rows x 1 unit column; this workgroup: 32 rows, 16 per pass
+    const FastItem it = fast_item(n_items, n_cb, cg_magic, cg_shift);
+    if (!it.valid) return;
     const uint32_t l = threadIdx.x & 15;
+    const uint32_t j = it.cg;
     uint4 w[kMxUnits];
-    uint32_t r[kMxUnits], off[kMxUnits], unit[kMxUnits];
+    uint32_t r[kMxUnits], off[kMxUnits];
 #pragma unroll
     for (int u = 0; u < kMxUnits; ++u) {
-        unit[u] = (blockIdx.x * kMxUnits + u) * (kThreads / 16) + (threadIdx.x >> 4);
-        r[u] = static_cast<uint32_t>((static_cast<uint64_t>(unit[u]) * magic) >> shift);
-        off[u] = r[u] * cols + 128 * (unit[u] - r[u] * n_cb) + 8 * l;
+        r[u] = it.tile * 128 + it.q * 32 + u * (kThreads / 16) + (threadIdx.x >> 4);
+        off[u] = r[u] * cols + 128 * j + 8 * l;
         w[u] = make_uint4(0u, 0u, 0u, 0u);
         if (r[u] < rows) w[u] = ld_stream16(x + off[u]);
     }
@@ -236,10 +263,7 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uin
         uint32_t word = e << (8 * (l >> 2));
         word |= dpp<0x124>(word);  // row_ror:4
         word |= dpp<0x128>(word);  // row_ror:8
-        if (l == 0 && unit[u] < n_units) {
-            const uint32_t j = unit[u] - r[u] * n_cb;
-            sc[(((r[u] >> 7) * n_cb + j) * 32 + (r[u] & 31)) * 4 + ((r[u] & 127) >> 5)] = word;
-        }
+        if (l == 0) sc[((it.tile * n_cb + j) * 32 + (r[u] & 31)) * 4 + it.q] = word;
     }
 }
 
@@ -248,9 +272,9 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uin
 //   s8 = E4M3(min(amax/6/g, 448)); T = g*s8; codes = E2M1(clamp(x/T, +-6)), T==0 -> +0.
 // Divisions are IEEE fp32 divisions, as in the reference's eager path.
 
-// Pack 8 values already clamped to [-6, 6] into E2M1 nibbles with the hardware convert
-// (RNE, identical to f_to_e2m1 on that range); the convert puts its first operand in
-// the low nibble.
+// Pack 8 non-NaN values into E2M1 nibbles with the hardware convert: RNE, identical to
+// f_to_e2m1 of the value clamped to [-6, 6] (the convert saturates), and the first
+// operand lands in the low nibble.
 template <bool HI_FIRST>
 __device__ __forceinline__ uint32_t pack_e2m1x8(const float* q) {
     const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of each pair that goes to the low nibble
@@ -276,7 +300,7 @@ __device__ __forceinline__ float x86_nan(float r, float a, float b) {
 
 // T = g * float(s8) with the reference's NaN bits
 __device__ __forceinline__ float nvfp4_total(float g, uint32_t s8) {
-    const float s = (s8 & 0x7fu) == 0x7fu ? as_f(0x7ff00000u | ((s8 & 0x80u) << 24)) : e4m3_to_f(s8);
+    const float s = (s8 & 0x7fu) == 0x7fu ? as_f(0x7ff00000u | ((s8 & 0x80u) << 24)) : hw_e4m3_to_f<0>(s8);
     return x86_nan(g * s, g, s);
 }
 
@@ -308,18 +332,32 @@ __device__ __forceinline__ uint32_t nvfp4_codes8_div(const float* v, float T) {
     return w;
 }
 
+// Out-of-line form for the fast kernel, which needs it only for rare blocks (values
+// passed in registers, so the call uses no scratch memory).
+template <bool HI_FIRST>
+__device__ __noinline__ uint32_t nvfp4_codes8_div_rare(float v0, float v1, float v2, float v3, float v4, float v5,
+                                                       float v6, float v7, float T) {
+    const float v[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+    return nvfp4_codes8_div<HI_FIRST>(v, T);
+}
+
 // Block scale code s8 from the block amax and the global scale (IEEE divisions).
 // A NaN c keeps the sign the reference's fp32 ops give it: the amax (a |x|) NaN is
 // positive and x86 division returns its first NaN operand, so NaN amax -> 0x7F, and
 // otherwise a NaN g passes its sign; fp32 clamp(max=448) returns the NaN unchanged.
-__device__ __forceinline__ uint32_t nvfp4_scale_code(float amax, float g) {
-    float c = (amax / 6.0f) / g;
+__device__ __forceinline__ uint32_t nvfp4_scale_code_of(float c, float amax, float g) {
     c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
     if (is_nan(c)) return is_nan(amax) || !is_nan(g) ? 0x7fu : (0x7fu | ((as_u(g) >> 24) & 0x80u));
     // 0 <= c <= 448 here (c < 0 only for g < 0, and clamp keeps it): the hardware
     // E4M3 convert is exact on [-448, 448]
     return hw_e4m3x4(c, 0.0f, 0.0f, 0.0f) & 0xffu;
 }
+__device__ __forceinline__ uint32_t nvfp4_scale_code(float amax, float g) {
+    return nvfp4_scale_code_of((amax / 6.0f) / g, amax, g);
+}
+// (amax / 6) / g out of line, for the fast kernel's rare blocks (inline, the compiler
+// if-converts it and executes both divisions on every block)
+__device__ __noinline__ float nvfp4_c_div_rare(float amax, float g) { return (amax / 6.0f) / g; }
 
 template <int IN, bool HI_FIRST>
 __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __restrict__ x,
@@ -356,40 +394,61 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 // ------------------------------------------------------- NVFP4, 16-bit fast path
 // For bf16/f16 inputs with no column padding, cols % 64 == 0, 16-byte aligned, < 2^31
 // elements.  One lane per 16-element block (two 16-byte streaming loads), four lanes
-// per unit (one scale word), two units per thread.  Per block, s8 and T are computed as
-// above; then y = RN(1/T) by one IEEE division and every element's quotient by one
-// Markstein correction step,
-//   q0 = v*y;  r = fma(-T, q0, v);  q = fma(r, y, q0) with the sign of v,
-// instead of an IEEE division per element.  The E2M1 code of clamp(q, +-6) equals that
-// of clamp(v/T, +-6) for every bf16 and every f16 v and every T: checked exhaustively
-// for all 2^23 significands of T in [1, 2) against all v in [2^-5, 2^5) (both signs),
-// which covers every code boundary; smaller |v| give code 0 and larger |v| code 7 on
-// both sides, and every step scales exactly by powers of two while T lies in
-// [2^-120, 2^120].  (v*y alone gets 516 bf16 and 3904 f16 codes wrong in that domain.)
-// Blocks whose amax is not finite or whose T lies outside that range, and every block
-// when g is not a positive normal float, use the IEEE division per element.
-constexpr int kNvUnits = 2;  // units per thread
+// per unit (one scale word), two units per thread.  The IEEE divisions of the
+// reference are replaced by Markstein correction steps, each exact:
+//   c = (amax / 6) / g:  c0 = amax*y6, c1 = fma(-fma(6, c0, -amax), y6, c0), then the
+//                        same step with y_g = RN(1/g) (one IEEE division per thread);
+//                        bit-identical to the two IEEE divisions for every bf16 / f16
+//                        amax significand and every g significand, checked exhaustively;
+//   q = v / T:           y = RN(1/T) (one IEEE division per block), q0 = v*y,
+//                        e = fma(T, q0, -v), q = fma(-e, y, q0); the E2M1 code of q
+//                        equals that of the IEEE quotient for every bf16 and f16 v
+//                        (both signs, and +-0) and every T significand: checked
+//                        exhaustively for T in [1, 2) and v in [2^-6, 2^5), which covers
+//                        every code boundary, as (v*y alone gets 516 bf16 and 3904 f16
+//                        codes wrong).  The negated residual keeps the sign of a zero v.
+// The steps scale exactly by powers of two while every intermediate stays normal and
+// finite, which the guards ensure: g and amax within [2^-60, 2^60] for the scale, and
+// for the codes c <= 448 (so |v/T| < 10) and T within [2^-120, 2^120]; other blocks use
+// the IEEE divisions.  The E2M1 convert saturates out-of-range inputs to +-6 exactly as
+// the reference's clamp (checked on all 2^32 non-NaN floats), so no clamp is needed.
+constexpr int kNvUnits = 2;  // units per thread: 2 passes cover a workgroup's 32 rows x G units
 
-template <int IN, bool HI_FIRST>
-__global__ __launch_bounds__(kThreads) void quantize_nvfp4_fast_kernel(const uint16_t* __restrict__ x,
-                                                                       const float* __restrict__ gptr,
-                                                                       uint8_t* __restrict__ qx,
-                                                                       uint32_t* __restrict__ sc, uint32_t rows,
-                                                                       uint32_t cols, uint32_t n_cb,
-                                                                       uint32_t n_units, uint32_t magic,
-                                                                       uint32_t shift) {
+// G = unit columns per item (4 or 16); the workgroup has 64*G threads.  A wave's 16
+// units in one pass are 16/G rows x G consecutive units, so with G = 16 each load
+// instruction reads 2 KB of one row.
+template <int IN, bool HI_FIRST, int G>
+__global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint16_t* __restrict__ x,
+                                                                     const float* __restrict__ gptr,
+                                                                     uint8_t* __restrict__ qx,
+                                                                     uint32_t* __restrict__ sc, uint32_t rows,
+                                                                     uint32_t cols, uint32_t n_cb, uint32_t n_items,
+                                                                     uint32_t n_cg, uint32_t cg_magic,
+                                                                     uint32_t cg_shift) {
+    // item: 128 rows x G unit columns.  This workgroup: rows 8q..8q+7 of each of the
+    // tile's four 32-row groups (32 rows) x G units.  Its scale words of one unit column
+    // are then 32 consecutive words (one 128-byte line): staged in LDS and stored as
+    // whole lines.
+    constexpr uint32_t kUnitsPerPass = 16 * G;
+    const FastItem it = fast_item(n_items, n_cg, cg_magic, cg_shift);
+    if (!it.valid) return;
+    __shared__ uint32_t sw[G][32];
     const uint32_t l = threadIdx.x & 3;
     const float g = gptr[0];
-    const bool g_ok = g >= 0x1p-126f && g < __builtin_inff();  // false for NaN
+    const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
+    const float yg = 1.0f / g;
+    constexpr float y6 = 1.0f / 6.0f;
     uint4 w[kNvUnits][2];
-    uint32_t r[kNvUnits], off[kNvUnits], unit[kNvUnits];
+    uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits];
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
-        unit[u] = (blockIdx.x * kNvUnits + u) * (kThreads / 4) + (threadIdx.x >> 2);
-        r[u] = static_cast<uint32_t>((static_cast<uint64_t>(unit[u]) * magic) >> shift);
-        off[u] = r[u] * cols + 64 * (unit[u] - r[u] * n_cb) + 16 * l;
+        const uint32_t ul = u * kUnitsPerPass + (threadIdx.x >> 2);  // unit in the workgroup
+        const uint32_t rs = ul / G;                                  // row slot: 8 rows x 4 groups
+        r[u] = it.tile * 128 + (rs & 3) * 32 + it.q * 8 + (rs >> 2);
+        j[u] = it.cg * G + ul % G;
+        off[u] = r[u] * cols + 64 * j[u] + 16 * l;
         w[u][0] = w[u][1] = make_uint4(0u, 0u, 0u, 0u);
-        if (r[u] < rows) {
+        if (r[u] < rows && j[u] < n_cb) {
             w[u][0] = ld_stream16(x + off[u]);
             w[u][1] = ld_stream16(x + off[u] + 8);
         }
@@ -397,34 +456,51 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_fast_kernel(const uin
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
-        const uint32_t s8 = r[u] < rows ? nvfp4_scale_code(amax, g) : 0u;
+        float c;
+        if (g_ok && amax >= 0x1p-60f && amax <= 0x1p60f) {
+            const float c0 = amax * y6;
+            const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
+            const float d0 = c1 * yg;
+            c = __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
+        } else {
+            c = nvfp4_c_div_rare(amax, g);
+        }
+        const uint32_t s8 = r[u] < rows ? nvfp4_scale_code_of(c, amax, g) : 0u;
         const float T = nvfp4_total(g, s8);
         float v[16];
         unpack16x8<IN>(w[u][0], *reinterpret_cast<float(*)[8]>(&v[0]));
         unpack16x8<IN>(w[u][1], *reinterpret_cast<float(*)[8]>(&v[8]));
         uint2 codes = make_uint2(0u, 0u);
         if (T != 0.0f) {
-            if (g_ok && amax < __builtin_inff() && T >= 0x1p-120f && T <= 0x1p120f) {
+            if (c <= 448.0f && T >= 0x1p-120f && T <= 0x1p120f) {
                 const float y = 1.0f / T;
                 float q[16];
 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
                     const float q0 = v[t] * y;
-                    const float e = __builtin_fmaf(-T, q0, v[t]);
-                    q[t] = __builtin_amdgcn_fmed3f(__builtin_copysignf(__builtin_fmaf(e, y, q0), v[t]), -6.0f, 6.0f);
+                    const float e = __builtin_fmaf(T, q0, -v[t]);
+                    q[t] = __builtin_fmaf(-e, y, q0);
                 }
                 codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
             } else {
-                codes = make_uint2(nvfp4_codes8_div<HI_FIRST>(&v[0], T), nvfp4_codes8_div<HI_FIRST>(&v[8], T));
+                codes = make_uint2(
+                    nvfp4_codes8_div_rare<HI_FIRST>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], T),
+                    nvfp4_codes8_div_rare<HI_FIRST>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15], T));
             }
         }
-        if (r[u] < rows) *reinterpret_cast<uint2*>(qx + off[u] / 2) = codes;
+        if (r[u] < rows && j[u] < n_cb) *reinterpret_cast<uint2*>(qx + off[u] / 2) = codes;
         uint32_t word = s8 << (8 * l);
         word |= dpp<0xB1>(word);  // quad_perm [1,0,3,2]
         word |= dpp<0x4E>(word);  // quad_perm [2,3,0,1]
-        if (l == 0 && unit[u] < n_units) {
-            const uint32_t j = unit[u] - r[u] * n_cb;
-            sc[(((r[u] >> 7) * n_cb + j) * 32 + (r[u] & 31)) * 4 + ((r[u] & 127) >> 5)] = word;
+        // word (r, j) sits at ((tile*n_cb + j)*32 + (r & 31))*4 + (r & 127)/32
+        if (l == 0) sw[j[u] % G][((r[u] & 31) - it.q * 8) * 4 + ((r[u] & 127) >> 5)] = word;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8 * G) {
+        const uint32_t jj = threadIdx.x >> 3, part = threadIdx.x & 7, jc = it.cg * G + jj;
+        if (jc < n_cb) {
+            const uint4 v = *reinterpret_cast<const uint4*>(&sw[jj][part * 4]);
+            *reinterpret_cast<uint4*>(sc + (it.tile * n_cb + jc) * 128 + it.q * 32 + part * 4) = v;
         }
     }
 }
@@ -527,19 +603,21 @@ extern "C" int ckh_quantize_mxfp8(const void* x, void* qx, void* scales, int64_t
     uint8_t* q = static_cast<uint8_t*>(qx);
     uint32_t* s = static_cast<uint32_t*>(scales);
     if ((in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 128 == 0 &&
-        aligned(x, 16) && rows * cols < (int64_t(1) << 31) && n_units * 16 + 4 * kThreads * kMxUnits < (int64_t(1) << 31)) {
+        aligned(x, 16) && rup(rows, 128) * cols < (int64_t(1) << 31)) {
+        // items: 128-row tiles x unit columns (one unit each), 4 workgroups per item
+        const int64_t n_items = cdiv(rows, 128) * n_cb;
         uint32_t magic, shift;
         magic_div(n_cb, magic, shift);
-        dim3 fgrid(static_cast<unsigned>(cdiv(n_units * 16, kThreads * kMxUnits)));
+        dim3 fgrid(static_cast<unsigned>(cdiv(n_items, 8) * 32));
         const uint16_t* xx = static_cast<const uint16_t*>(x);
         const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
-                   n32 = static_cast<uint32_t>(n_cb), u32 = static_cast<uint32_t>(n_units);
+                   n32 = static_cast<uint32_t>(n_cb), i32 = static_cast<uint32_t>(n_items);
         if (in_code == CKH_BF16)
             hipLaunchKernelGGL((quantize_mxfp8_fast_kernel<CKH_BF16>), fgrid, dim3(kThreads), 0, st, xx, q, s, r32,
-                               c32, n32, u32, magic, shift);
+                               c32, n32, i32, magic, shift);
         else
             hipLaunchKernelGGL((quantize_mxfp8_fast_kernel<CKH_F16>), fgrid, dim3(kThreads), 0, st, xx, q, s, r32,
-                               c32, n32, u32, magic, shift);
+                               c32, n32, i32, magic, shift);
         return check_launch("quantize_mxfp8");
     }
     dim3 grid(static_cast<unsigned>(cdiv(n_units * 16, kThreads)));
@@ -574,24 +652,34 @@ extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void*
     uint32_t* s = static_cast<uint32_t*>(scales);
     const bool hf = hi_first != 0;
     if ((in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 64 == 0 &&
-        aligned(x, 16) && aligned(qx, 8) && rows * cols < (int64_t(1) << 31) &&
-        n_units * 4 + 4 * kThreads * kNvUnits < (int64_t(1) << 31)) {
+        aligned(x, 16) && aligned(qx, 8) && aligned(scales, 16) && rup(rows, 128) * cols < (int64_t(1) << 31)) {
+        // items: 128-row tiles x groups of G unit columns, 4 workgroups per item; G = 16
+        // (2 KB row runs) unless a row has fewer than 16 units
+        const int G = n_cb >= 16 ? 16 : 4;
+        const int64_t n_cg = cdiv(n_cb, G), n_items = cdiv(rows, 128) * n_cg;
         uint32_t magic, shift;
-        magic_div(n_cb, magic, shift);
-        dim3 fgrid(static_cast<unsigned>(cdiv(n_units * 4, kThreads * kNvUnits)));
+        magic_div(n_cg, magic, shift);
+        dim3 fgrid(static_cast<unsigned>(cdiv(n_items, 8) * 32));
         const uint16_t* xx = static_cast<const uint16_t*>(x);
         const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
-                   n32 = static_cast<uint32_t>(n_cb), u32 = static_cast<uint32_t>(n_units);
-#define LAUNCH_FAST(I, H)                                                                                          \
-    hipLaunchKernelGGL((quantize_nvfp4_fast_kernel<I, H>), fgrid, dim3(kThreads), 0, st, xx, g, q, s, r32, c32, n32, \
-                       u32, magic, shift)
+                   n32 = static_cast<uint32_t>(n_cb), i32 = static_cast<uint32_t>(n_items),
+                   g32 = static_cast<uint32_t>(n_cg);
+#define LAUNCH_FAST(I, H, GG)                                                                                     \
+    hipLaunchKernelGGL((quantize_nvfp4_fast_kernel<I, H, GG>), fgrid, dim3(64 * GG), 0, st, xx, g, q, s, r32, c32, \
+                       n32, i32, g32, magic, shift)
+#define BY_G(I, H)                     \
+    do {                               \
+        if (G == 16) LAUNCH_FAST(I, H, 16); \
+        else LAUNCH_FAST(I, H, 4);          \
+    } while (0)
         if (in_code == CKH_BF16) {
-            if (hf) LAUNCH_FAST(CKH_BF16, true);
-            else LAUNCH_FAST(CKH_BF16, false);
+            if (hf) BY_G(CKH_BF16, true);
+            else BY_G(CKH_BF16, false);
         } else {
-            if (hf) LAUNCH_FAST(CKH_F16, true);
-            else LAUNCH_FAST(CKH_F16, false);
+            if (hf) BY_G(CKH_F16, true);
+            else BY_G(CKH_F16, false);
         }
+#undef BY_G
 #undef LAUNCH_FAST
         return check_launch("quantize_nvfp4");
     }

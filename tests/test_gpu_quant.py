@@ -198,7 +198,8 @@ def _check_nv(x, g, pad, hi_first=True):
 
 @pytest.mark.parametrize("hi_first", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (16, 64), (130, 192), (1, 64), (257, 320)])
+@pytest.mark.parametrize("m,k", [(1024, 2048), (512, 1024), (128, 256), (16, 64), (130, 192), (1, 64), (257, 320),
+                                 (130, 1600)])
 def test_quantize_nvfp4(dtype, m, k, hi_first, hip, seed):
     x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1))).to(dtype)
     x[0, :16] = 0
@@ -220,6 +221,7 @@ def test_quantize_nvfp4_special_blocks(dtype, hi_first, hip, seed):
     x[5, 40] = float("inf")
     x[6, 48:64] = float("-inf")
     x[7, :16] = 1e-30
+    x[9, 16:32] = 3e25  # amax above the fast scale path's range
     # one block whose amax gives T = g * 6 exactly: every boundary multiple of T/6
     x[8, :16] = torch.tensor([6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5.0, 0.5])
     x = x.to(dtype)
