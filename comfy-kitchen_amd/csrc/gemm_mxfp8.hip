@@ -36,7 +36,9 @@
 // of 32 consecutive rows) conflict-free for both 32- and 64-bank LDS layouts.
 // Workgroups are dispatched round-robin over the 8 XCDs; the tile index is remapped
 // so each XCD walks a contiguous range of tiles (column-major over m), keeping the
-// tiles that share a weight panel on one L2.
+// tiles that share a weight panel on one L2.  Tiles run one per CU in rounds; when the
+// last round would be at most half full, its tiles go to a second launch as 256 x 128
+// half tiles (2 MFMA columns per wave, 8-slot stages) on twice as many CUs.
 #include <type_traits>
 #include <utility>
 
@@ -108,15 +110,17 @@ struct Args {
     int M, N, K;
     int ncb;               // scale column blocks: ceil(K/32/4)
     int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
-    int tiles_m, tiles_n;
+    int tiles_m, tiles_n;  // 256 x 256 tile grid
+    int tile_base;         // first tile of this launch (linear, column-major over m)
+    int n_tiles;           // tiles in this launch (half-width launches: 2 workgroups per tile)
     // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
     const float* tsa;
     const float* tsb;
 };
 
 // Register-staged loads of one operand for a pair of stages (s, s + 1), i.e. K bytes
-// [k0, k0 + 128) of the tile's 256 rows.  Wave w, load j (0..7) covers rows
-// R = 64 w + 8 j .. +7: lane i fetches 16-byte chunk c = i % 8 of row R + i / 8, so each
+// [k0, k0 + 128) of the tile's 256 (or 128) rows.  Wave w, load j (0..7, or 0..3)
+// covers rows R = 64 w + 8 j .. +7 (R = 32 w + 8 j for 128 rows): lane i fetches 16-byte chunk c = i % 8 of row R + i / 8, so each
 // 8 lanes read one whole 128-byte line (with all CUs loading, half-line requests reach
 // only ~70% of the L2 throughput of whole lines).  Chunks 0..3 go to stage s's buffer,
 // 4..7 to stage s + 1's, at physical chunk (c % 4) ^ swz(row); swz(row + 8) = swz(row) ^ 1.
@@ -130,10 +134,11 @@ struct Loader {
     bool hi;            // chunk belongs to stage s + 1
 };
 
-__device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int K, int wave, int lane) {
+__device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int K, int wave, int lane,
+                                             int rows_per_wave = 64) {
     Loader L;
     L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * K);
-    const int row = 64 * wave + (lane >> 3), c = lane & 7;
+    const int row = rows_per_wave * wave + (lane >> 3), c = lane & 7;
     L.cbyte = c << 4;
     L.voff = static_cast<uint32_t>(row * K + L.cbyte);
     L.rowstep = 8u * K;
@@ -167,8 +172,9 @@ __device__ __forceinline__ void load_pair(const Loader& L, v4u (&x)[8], int k0, 
     (load_piece<J>(L, x, add), ...);
 }
 
+template <int NP = 8>
 __device__ __forceinline__ void load_pair(const Loader& L, v4u (&x)[8], int k0, int K) {
-    load_pair(L, x, k0, K, std::make_integer_sequence<int, 8>{});
+    load_pair(L, x, k0, K, std::make_integer_sequence<int, NP>{});
 }
 
 template <int... J>
@@ -177,8 +183,9 @@ __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], u
     (store_piece<J>(L, x, tx, ty), ...);
 }
 
+template <int NP = 8>
 __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], uint8_t* tx, uint8_t* ty) {
-    store_pair(L, x, tx, ty, std::make_integer_sequence<int, 8>{});
+    store_pair(L, x, tx, ty, std::make_integer_sequence<int, NP>{});
 }
 
 // Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
@@ -209,9 +216,10 @@ __device__ __forceinline__ void store_scales(const ScaleWords& S, uint8_t* sx, u
     *reinterpret_cast<uint32_t*>(sy + off + 256) = S.s1;
 }
 
+template <int NW>
 struct Frags {
-    v8i b[4];  // weight fragments (MFMA operand 0)
-    v8i a[4];  // activation fragments (MFMA operand 1)
+    v8i b[NW];  // weight fragments (MFMA operand 0)
+    v8i a[4];   // activation fragments (MFMA operand 1)
 };
 
 // Byte offsets (within an operand tile) of this lane's two 16-byte fragment halves
@@ -237,24 +245,14 @@ __device__ __forceinline__ v8i read_frag(const uint8_t* tile, const FragAddr& f)
     return r;
 }
 
-__device__ __forceinline__ void read_frags(Frags& F, const uint8_t* stage_buf, const FragAddr& fb,
+template <int NW>
+__device__ __forceinline__ void read_frags(Frags<NW>& F, const uint8_t* stage_buf, const FragAddr& fb,
                                            const FragAddr& fa) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        F.b[t] = read_frag(stage_buf + t * 32 * BK, fb);
+        if (t < NW) F.b[t] = read_frag(stage_buf + t * 32 * BK, fb);
         F.a[t] = read_frag(stage_buf + TILE + t * 32 * BK, fa);
     }
-}
-
-template <int OPSEL>
-__device__ __forceinline__ void mfma16(v16f (&acc)[4][4], const Frags& F, const uint32_t (&sb)[4],
-                                       const uint32_t (&sa)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.b[i], F.a[j], acc[i][j], 0, 0, OPSEL, sb[i],
-                                                                        OPSEL, sa[j]);
 }
 
 template <int OUT>
@@ -284,8 +282,13 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 
 // UNIT: per-tensor FP8 (TensorCoreFP8Layout): no block scales (every MFMA scale byte is
 // E8M0 127 = 1.0) and out = tsa * tsb * (A B^T) + bias.
-template <int OUT, int BIAS, bool UNIT>
+// NW: 32-column MFMA tiles per wave along n: 4 for 256 x 256 workgroup tiles, 2 for the
+// 256 x 128 half tiles that finish a grid whose last round would leave most CUs idle.
+template <int OUT, int BIAS, bool UNIT, int NW>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
+    constexpr int TBN = 64 * NW;  // tile width along n
+    constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
+    constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
     // Stage buffers 0, 1 and 2, 3 in two arrays.  Every stage reads fragments from one
     // array and writes staged data into the other, so the compiler knows they never
     // alias and may interleave the two freely; within an array, per-lane addresses of
@@ -293,11 +296,16 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
 
-    const int tiles = p.tiles_m * p.tiles_n;
+    // Workgroups are dispatched round-robin over the 8 XCDs; a full-tile launch remaps
+    // the index so each XCD walks a contiguous range of tiles (column-major over m),
+    // keeping the tiles that share a weight panel on one L2.  A half-tile launch gives
+    // tile L's two column halves to consecutive workgroups.
     int bid = blockIdx.x;
-    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-    const int tm = bid % p.tiles_m, tn = bid / p.tiles_m;
-    const int m0 = tm * BM, n0 = tn * BN;
+    if (NW == 4 && (p.n_tiles & 7) == 0) bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
+    const int L = p.tile_base + (NW == 4 ? bid : bid >> 1);
+    const int tm = L % p.tiles_m, tn = L / p.tiles_m;
+    const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
+    if (n0 >= p.N) return;  // a half tile wholly past N (uniform over the workgroup)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -305,17 +313,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     const int wm = wave & 1, wn = wave >> 1;
     const int half = lane >> 5, r32 = lane & 31;
 
-    const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * p.K, min(BN, p.N - n0), p.K, wave, lane);
+    const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * p.K, min(TBN, p.N - n0), p.K, wave, lane, TBN / 4);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * p.K, min(BM, p.M - m0), p.K, wave, lane);
     const __amdgpu_buffer_rsrc_t rssb = make_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = make_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
-    const FragAddr fab = make_frag_addr(wn * 128, lane);
+    const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
     const FragAddr faa = make_frag_addr(wm * 128, lane);
     const int KT = (p.K + BK - 1) / BK;
 
-    v16f acc[4][4];
+    v16f acc[NW][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NW; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
 
@@ -328,18 +336,20 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     v4u SB[8], SA[8];
     ScaleWords SW;
     auto load_b = [&](int s) {
-        load_pair(LB, SB, s * BK, p.K);
+        load_pair<PB>(LB, SB, s * BK, p.K);
         if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
     auto store_b = [&](auto x_c, auto y_c) {
-        store_pair(LB, SB, buf(x_c), buf(y_c));
+        store_pair<PB>(LB, SB, buf(x_c), buf(y_c));
         if constexpr (!UNIT) store_scales(SW, buf(x_c) + 2 * TILE, buf(y_c) + 2 * TILE, wave, lane);
     };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
     const int hs = 8 * half;
+    // the weight scale chunk holding this wave's n rows, and its first 32-row tile there
+    const int sbc = NW == 4 ? wn : 0, sbt = NW == 4 ? 0 : 2 * wn;
     auto read_scales = [&](auto b_c, uint32_t (&sb)[4], uint32_t (&sa)[4]) {
         if constexpr (UNIT) {
 #pragma unroll
@@ -347,17 +357,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             return;
         }
         const uint8_t* st = buf(b_c) + 2 * TILE;
-        const v4u wb = *reinterpret_cast<const v4u*>(st + wn * 512 + r32 * 16);
+        const v4u wb = *reinterpret_cast<const v4u*>(st + sbc * 512 + r32 * 16);
         const v4u wa = *reinterpret_cast<const v4u*>(st + STILE + wm * 512 + r32 * 16);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            sb[t] = wb[t] >> hs;
+            sb[t] = (NW == 4 ? wb[t] : (sbt ? wb[2 + (t & 1)] : wb[t & 1])) >> hs;
             sa[t] = wa[t] >> hs;
         }
     };
 
     uint32_t scb[4], sca[4];
-    Frags F0, F1;
+    Frags<NW> F0, F1;
 
     // Stage t held in buffer B = t % 4 (compile-time): fragments F (stage t) are in
     // registers; read stage t+1 into G.  A pair of stages (s, s+1), s even, moves in
@@ -370,7 +380,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     // no LDS latency is exposed), then its fragments in the order the next stage uses
     // them, and in slots 0..7 one staged chunk written to LDS followed by the load that
     // refills its registers, which therefore has a whole stage to arrive.
-    auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
+    auto stage = [&](auto b_c, int t, Frags<NW>& F, Frags<NW>& G) {
         constexpr int B = decltype(b_c)::value;
         constexpr bool EVEN = (B & 1) == 0;
         constexpr int OPSEL = EVEN ? 0 : 2;
@@ -390,36 +400,36 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.b[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
                                                                         OPSEL, sca[j]);
             if constexpr (k == 0 && !UNIT) {
-                wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + wn * 512 + r32 * 16);
+                wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + sbc * 512 + r32 * 16);
                 wa = *reinterpret_cast<const v4u*>(nx + 2 * TILE + STILE + wm * 512 + r32 * 16);
             }
             if constexpr (k == 1) G.a[0] = read_frag(nx + TILE, faa);
             if constexpr (k == 2) G.b[0] = read_frag(nx, fab);
             if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
-            if constexpr (k >= 6 && k <= 8) G.b[k - 5] = read_frag(nx + (k - 5) * 32 * BK, fab);
+            if constexpr (k >= 6 && k <= 4 + NW) G.b[k - 5] = read_frag(nx + (k - 5) * 32 * BK, fab);
             if constexpr (k < 8) {
                 if constexpr (EVEN) {
-                    store_piece<k>(LB, SB, wx, wy);
+                    if constexpr (k < PB) store_piece<k>(LB, SB, wx, wy);
                     load_piece<k>(LA, SA, add);
                 } else {
                     store_piece<k>(LA, SA, wx, wy);
-                    load_piece<k>(LB, SB, add);
+                    if constexpr (k < PB) load_piece<k>(LB, SB, add);
                 }
             }
-            if constexpr (k == 8 && !UNIT) {
+            if constexpr (k == (SLOTS > 8 ? 8 : SLOTS - 1) && !UNIT) {
                 if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
                 else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
             }
-            if constexpr (k == 12) {
+            if constexpr (k == SLOTS - 4) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    nb[u] = UNIT ? 0x7f7f7f7fu : wb[u] >> hs;
+                    nb[u] = UNIT ? 0x7f7f7f7fu : (NW == 4 ? wb[u] : (sbt ? wb[2 + (u & 1)] : wb[u & 1])) >> hs;
                     na[u] = UNIT ? 0x7f7f7f7fu : wa[u] >> hs;
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
         };
-        for_each_index(slot, std::make_integer_sequence<int, 16>{});
+        for_each_index(slot, std::make_integer_sequence<int, SLOTS>{});
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             scb[u] = nb[u];
@@ -471,10 +481,10 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
         for (int j = 0; j < 4; ++j) {
             uint8_t* rowp = slab(wm * 2 + (j >> 1)) + ((j & 1) * 32 + r32) * EPI_ROW;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NW; ++i) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int nl = wn * 128 + i * 32 + 8 * g + 4 * half;
+                    const int nl = wn * 32 * NW + i * 32 + 8 * g + 4 * half;
                     const int n = n0 + nl;
                     float v[4];
 #pragma unroll
@@ -488,13 +498,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             }
         }
         __syncthreads();
-        const uint8_t* src = slab(wave) + lane * 8;
-        const int n = n0 + 4 * lane;
+        // a row of the tile is TBN * 2 bytes: 64 lanes x 8 bytes (NW = 4) or 32 lanes x 8
+        // bytes with the wave's two halves on consecutive rows (NW = 2)
+        constexpr int LPR = TBN / 4;  // lanes per output row
+        const int lr = lane % LPR, lrow = lane / LPR;
+        const uint8_t* src = slab(wave) + lrow * EPI_ROW + lr * 8;
+        const int n = n0 + 4 * lr;
         const bool vec = (p.N & 3) == 0 && n + 4 <= p.N;
-        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64) * p.N + n;
-        const int rows = min(64, p.M - (m0 + wave * 64));
+        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64 + lrow) * p.N + n;
+        const int rows = min(64, p.M - (m0 + wave * 64)) - lrow;
 #pragma unroll 8
-        for (int rl = 0; rl < 64; ++rl) {
+        for (int rl = 0; rl < 64; rl += 64 / LPR) {
             const uint2 d = *reinterpret_cast<const uint2*>(src + rl * EPI_ROW);
             if (rl >= rows) break;
             uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
@@ -512,10 +526,10 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             const int m = m0 + wm * 128 + j * 32 + r32;
             if (m >= p.M) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NW; ++i) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int n = n0 + wn * 128 + i * 32 + 8 * g + 4 * half;
+                    const int n = n0 + wn * 32 * NW + i * 32 + 8 * g + 4 * half;
                     float v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * g + e], n + e);
@@ -540,10 +554,12 @@ using namespace ckh;
 
 namespace {
 
-template <bool UNIT>
-int launch_gemm(const mx::Args& p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT>), grid, dim3(mx::NT), 0, st, p)
+// Workgroups that can hold a 256 x 256 tile at once: one per CU.
+constexpr int kGemmSlots = 256;
+
+template <bool UNIT, int NW>
+void launch_part(const mx::Args& p, unsigned wgs, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT, NW>), dim3(wgs), dim3(mx::NT), 0, st, p)
 #define BY_BIAS(O)                                         \
     do {                                                   \
         if (!has_bias) LAUNCH(O, -1);                      \
@@ -556,6 +572,24 @@ int launch_gemm(const mx::Args& p, int out_code, int bias_code, bool has_bias, h
     else BY_BIAS(CKH_F32);
 #undef BY_BIAS
 #undef LAUNCH
+}
+
+// The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
+// half full (e.g. 864 tiles = 3 rounds + 96), its tiles are launched separately as
+// twice as many 256 x 128 half tiles, which finish in about 55% of a full tile's time.
+template <bool UNIT>
+int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : 0;
+    const int split = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
+    p.tile_base = 0;
+    p.n_tiles = tiles - split;
+    launch_part<UNIT, 4>(p, static_cast<unsigned>(p.n_tiles), out_code, bias_code, has_bias, st);
+    if (split) {
+        p.tile_base = tiles - split;
+        p.n_tiles = split;
+        launch_part<UNIT, 2>(p, static_cast<unsigned>(2 * split), out_code, bias_code, has_bias, st);
+    }
     return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }
 

@@ -67,6 +67,22 @@ def test_scaled_mm_mxfp8_extreme_scales(hip):
     assert d.abs().max().item() <= 5e-4
 
 
+@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float32, True)])
+def test_scaled_mm_mxfp8_half_tile_tail(out_dtype, with_bias, hip):
+    """289 tiles of 256 x 256: 256 run as full tiles, the last 33 as 66 half-width tiles
+    (one of them wholly past N, one partial)."""
+    m, n, k = 4352, 4196, 128
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=21)
+    bias = (torch.randn(n) * 2).float() if with_bias else None
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(),
+                             bias=None if bias is None else bias.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+    # the half tiles cover column-major tiles 256..288: tile column 15 (rows 256..) and 16
+    assert rel_l2(got[:, 15 * 256:], want[:, 15 * 256:]) <= REL_L2[out_dtype]
+
+
 def test_scaled_mm_mxfp8_config4_full(hip):
     """Config 4 at full size against a GPU fp32 matmul of the (bit-exact) dequantized operands."""
     import bench
