@@ -418,23 +418,37 @@ def _pmc_dispatches(d: Path, counter: str):
     return rows
 
 
+# kernel-name substring of each op's own dispatches (an op may launch several per call)
+OP_KERNELS = {"quantize_per_tensor_fp8": "ckh::quantize_fp8", "dequantize_per_tensor_fp8": "ckh::dequantize_fp8",
+              "apply_rope": "ckh::rope", "apply_rope1": "ckh::rope", "quantize_mxfp8": "ckh::quantize_mxfp8",
+              "scaled_mm_mxfp8": "ckh::mx::gemm", "quantize_nvfp4": "ckh::quantize_nvfp4",
+              "scaled_mm_nvfp4": "ckh::nv::gemm"}
+
+
 def summarize_pmc(fetch_dir: str, write_dir: str, configs, command: str):
     """HBM bytes per launch of each op: counter KiB scaled by calibration bytes / calibration KiB."""
     seq = [n for n, _ in pmc_sequence_names(configs)]
     out = {"bytes_per_launch": {}, "calibration": {}, "command": command}
     for key, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
         rows = _pmc_dispatches(Path(d), counter)
-        n = len(seq) * PMC_CALLS
-        ours = [i for i, r in enumerate(rows) if "ckh::" in r[1]]  # the ops' own kernels
-        ops = [rows[i] for i in ours[-n:]]
-        # calibration: the largest non-ckh dispatch just before the measured sequence
-        calib = max((r for r in rows[max(0, ours[-n] - 3):ours[-n]] if "ckh::" not in r[1]), key=lambda r: r[2])
+        # calibration: the largest non-ckh dispatch; the measured sequence follows it
+        ci = max((i for i, r in enumerate(rows) if "ckh::" not in r[1]), key=lambda i: rows[i][2])
+        calib = rows[ci]
         factor = PMC_CALIB_BYTES / (calib[2] * 1024.0)
         out["calibration"][counter] = {"kernel": calib[1][:60], "kib": calib[2], "factor": round(factor, 4)}
-        for i, name in enumerate(seq):
-            vals = [v for _, _, v in ops[i * PMC_CALLS:(i + 1) * PMC_CALLS]]
-            b = sum(vals) / len(vals) * 1024.0 * factor
+        ours = [r for r in rows[ci + 1:] if "ckh::" in r[1]]  # the ops' own kernels, in order
+        i = 0
+        for name in seq:
+            sub, run = OP_KERNELS[name], []
+            # apply_rope and apply_rope1 share a kernel (one dispatch per call each)
+            cap = PMC_CALLS if name.startswith("apply_rope") else len(ours)
+            while i < len(ours) and sub in ours[i][1] and len(run) < cap:
+                run.append(ours[i][2])
+                i += 1
+            assert run, f"no dispatches of {name} in the counter run"
+            b = sum(run) / PMC_CALLS * 1024.0 * factor
             out["bytes_per_launch"].setdefault(name, {})[key] = round(b)
+            out["bytes_per_launch"][name]["dispatches_per_call"] = len(run) // PMC_CALLS
     for name, v in out["bytes_per_launch"].items():
         v["total"] = v.get("fetch", 0) + v.get("write", 0)
     (REPO / "profiles").mkdir(exist_ok=True)
