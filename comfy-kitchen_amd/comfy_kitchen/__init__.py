@@ -48,6 +48,16 @@ __all__ = [
 ]
 
 
+def amax_scale(x: torch.Tensor, divisor: float) -> torch.Tensor:
+    """amax(|x|) / divisor computed in x's dtype, returned as a 0-dim fp32 device tensor.
+
+    Not part of the reference's public API: it is the default scale of the layouts'
+    quantize (reference tensor/fp8.py:56-61, tensor/nvfp4.py:64-69) as one device-side
+    reduction, so dynamic quantization needs no host round trip.
+    """
+    return torch.ops.comfy_kitchen.amax_scale(x, float(divisor))
+
+
 def quantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
                             output_type: torch.dtype = torch.float8_e4m3fn) -> torch.Tensor:
     """FP8 quantize with one fp32 scale: fp8(clamp(x * (1/scale), +-max))."""

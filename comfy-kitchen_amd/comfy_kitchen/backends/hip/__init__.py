@@ -24,6 +24,7 @@ from ...float_utils import roundup
 from ...ops import DTYPE_TO_CODE
 
 __all__ = [
+    "amax_scale",
     "apply_rope",
     "apply_rope1",
     "dequantize_mxfp8",
@@ -56,8 +57,9 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_scaled_mm_mxfp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_fp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
+    "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib: ctypes.CDLL | None = None
 
@@ -150,6 +152,19 @@ def dequantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
     with _on_device(x):
         _call("ckh_dequantize_fp8", x.data_ptr(), s.data_ptr(), out.data_ptr(), x.numel(),
               DTYPE_TO_CODE[x.dtype], DTYPE_TO_CODE[output_type], _stream(x))
+    return out
+
+
+def amax_scale(x: torch.Tensor, divisor: float) -> torch.Tensor:
+    """amax(|x|) / divisor computed in x's dtype, as a 0-dim fp32 tensor on x's device
+    (the layouts' default scale, reference tensor/fp8.py:56-61, tensor/nvfp4.py:64-69)."""
+    x = x.contiguous()
+    if x.numel() == 0:
+        raise RuntimeError("amax_scale: empty tensor")
+    out = torch.empty((), dtype=torch.float32, device=x.device)
+    with _on_device(x):
+        _call("ckh_amax_scale", x.data_ptr(), x.numel(), DTYPE_TO_CODE[x.dtype], float(divisor), out.data_ptr(),
+              _stream(x))
     return out
 
 
@@ -359,6 +374,7 @@ def _build_constraints() -> dict:
 
     two_d = (ExactDims(2),)
     return {
+        "amax_scale": fc(x=ParamConstraint(dtypes=floats)),
         "quantize_per_tensor_fp8": fc(x=ParamConstraint(dtypes=floats), scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
                                       output_type=ParamConstraint(dtypes=fp8)),
         "dequantize_per_tensor_fp8": fc(x=ParamConstraint(dtypes=fp8), scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),

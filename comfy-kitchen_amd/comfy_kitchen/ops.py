@@ -99,6 +99,17 @@ def _(a, b, tensor_scale_a, tensor_scale_b, block_scale_a, block_scale_b, bias, 
     return torch.empty((a.shape[0], b.shape[0]), dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code], device=a.device)
 
 
+# ------------------------------------------------------------- dynamic scales
+@torch.library.custom_op("comfy_kitchen::amax_scale", mutates_args=())
+def amax_scale(x: torch.Tensor, divisor: float) -> torch.Tensor:
+    return _dispatch("amax_scale", x=x, divisor=divisor)
+
+
+@amax_scale.register_fake
+def _(x, divisor):
+    return torch.empty((), dtype=torch.float32, device=x.device)
+
+
 # ------------------------------------------------------------------------ MXFP8
 @torch.library.custom_op("comfy_kitchen::quantize_mxfp8", mutates_args=())
 def quantize_mxfp8(x: torch.Tensor, pad_32x: bool) -> tuple[torch.Tensor, torch.Tensor]:

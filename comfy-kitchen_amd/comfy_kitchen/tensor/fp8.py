@@ -39,7 +39,8 @@ class TensorCoreFP8Layout(QuantizedLayout):
         import comfy_kitchen as ck
 
         if scale is None or (isinstance(scale, str) and scale == "recalculate"):
-            scale = torch.amax(tensor.abs()) / torch.finfo(dtype).max
+            # amax(|x|) / max in x's dtype, as one device-side reduction
+            scale = ck.amax_scale(tensor, torch.finfo(dtype).max)
         if not isinstance(scale, torch.Tensor):
             scale = torch.tensor(scale)
         scale = scale.to(device=tensor.device, dtype=torch.float32)

@@ -51,7 +51,8 @@ class TensorCoreNVFP4Layout(QuantizedLayout):
         if tensor.dim() != 2:
             raise ValueError(f"NVFP4 requires 2D tensor, got {tensor.dim()}D")
         if scale is None or (isinstance(scale, str) and scale == "recalculate"):
-            scale = torch.amax(tensor.abs()) / (F8_E4M3_MAX * F4_E2M1_MAX)
+            # amax(|x|) / max in x's dtype, as one device-side reduction
+            scale = ck.amax_scale(tensor, (F8_E4M3_MAX * F4_E2M1_MAX))
         if not isinstance(scale, torch.Tensor):
             scale = torch.tensor(scale)
         scale = scale.to(device=tensor.device, dtype=torch.float32)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 1
+#define CKH_ABI_VERSION 2
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -166,6 +166,19 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
                         const void* alpha, const void* bias, void* out, int64_t M,
                         int64_t N, int64_t K, int out_code, int bias_code,
                         uintptr_t stream);
+
+/*
+ * Dynamic per-tensor scale: *scale_out = float(round_x(amax(|x|) / divisor)), the amax
+ * and the quotient rounded to x's dtype (in_code), as the layouts' default scale
+ * torch.amax(tensor.abs()) / max computes it.  x: numel contiguous elements; scale_out:
+ * one f32 on device, used as the reduction's scratch word, so no allocation.  A NaN in
+ * x gives a NaN scale.  Replaces that torch expression in TensorCoreFP8Layout.quantize
+ * (tensor/fp8.py:56-61, divisor 448) and TensorCoreNVFP4Layout.quantize
+ * (tensor/nvfp4.py:64-69, divisor 2688); the result feeds ckh_quantize_fp8 /
+ * ckh_quantize_nvfp4 on the same stream without a host round trip.
+ */
+int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
+                   uintptr_t stream);
 
 #ifdef __cplusplus
 }

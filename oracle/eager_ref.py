@@ -70,6 +70,12 @@ def e8m0_to_f32(x: torch.Tensor) -> torch.Tensor:
 
 
 # ------------------------------------------------------------- per-tensor FP8
+def default_scale(x: torch.Tensor, max_value: float) -> torch.Tensor:
+    """The layouts' default per-tensor scale (tensor/fp8.py:56-61, tensor/nvfp4.py:64-69):
+    torch.amax(x.abs()) / max_value in x's dtype, then cast to fp32 (a 0-dim tensor)."""
+    return (torch.amax(x.abs()) / max_value).to(torch.float32)
+
+
 def quantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
                             output_type: torch.dtype = torch.float8_e4m3fn) -> torch.Tensor:
     lp_max = F8_E4M3_MAX if output_type == torch.float8_e4m3fn else F8_E5M2_MAX

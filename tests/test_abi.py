@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 1
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 2
 
 
 def test_invalid_arguments_return_error(lib):

@@ -273,3 +273,40 @@ def test_dequantize_nvfp4(out_dtype, hi_first, hip, seed):
     want = ref.dequantize_nvfp4(q, g, s, out_dtype, hi_first=hi_first)
     got = ck.dequantize_nvfp4(q.cuda(), g.cuda(), s.cuda(), out_dtype, hi_first=hi_first)
     assert torch.equal(bits(got), bits(want))
+
+
+# ------------------------------------------------------------ dynamic scales
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003, 4096 * 3072])
+@pytest.mark.parametrize("divisor", [448.0, 2688.0])
+def test_amax_scale_matches_torch(dtype, n, divisor, hip, seed):
+    x = (torch.randn(n) * torch.exp(torch.randn(1) * 3)).to(dtype)
+    want = ref.default_scale(x, divisor)
+    got = ck.amax_scale(x.cuda(), divisor)
+    assert got.shape == () and got.dtype == torch.float32
+    assert torch.equal(got.cpu().view(torch.int32), want.view(torch.int32))
+
+
+def test_amax_scale_misaligned_nan_and_sign(hip, seed):
+    x = torch.randn(4099).bfloat16()
+    x[1000] = -1234.5  # the amax is taken of |x|
+    got = ck.amax_scale(x.cuda()[3:], 448.0)  # a view 6 bytes into the buffer
+    assert torch.equal(got.cpu(), ref.default_scale(x[3:], 448.0))
+    x[77] = float("nan")
+    assert torch.isnan(ck.amax_scale(x.cuda(), 448.0)).item()
+
+
+@pytest.mark.parametrize("layout", ["TensorCoreFP8Layout", "TensorCoreNVFP4Layout"])
+def test_layout_dynamic_scale_uses_the_reference_default(layout, hip, seed):
+    from comfy_kitchen.tensor import QuantizedTensor
+
+    x = (torch.randn(256, 512) * 3).bfloat16()
+    qt = QuantizedTensor.from_float(x.cuda(), layout)
+    want = ref.default_scale(x, 448.0 if layout == "TensorCoreFP8Layout" else 2688.0)
+    assert torch.equal(qt._params.scale.reshape(()).cpu(), want)
+    if layout == "TensorCoreFP8Layout":
+        _fp8_equal(qt._qdata, ref.quantize_per_tensor_fp8(x, want.reshape(1)))
+    else:
+        q, s = ref.quantize_nvfp4(x, want.reshape(1))
+        assert torch.equal(qt._qdata.cpu(), q)
+        assert torch.equal(bits(qt._params.block_scale), bits(s))
