@@ -262,4 +262,29 @@ __device__ __forceinline__ float load1(const void* p, int64_t i) {
 template <int C>
 struct ElemSize { static constexpr int value = (C == CKH_F32) ? 4 : 2; };
 
+// ------------------------------------------------------------ GEMM tile order
+// Tile L of a tiles_m x tiles_n output-tile grid in grouped order: groups of
+// kTileGroup tile rows (m), each group walked column by column.  The GEMMs hand each
+// XCD a contiguous run of L per round (32 tiles on 32 CUs); in grouped order such a run
+// is a compact ~6 x 5 block of tiles, which touches ~12 operand panels instead of the
+// ~20 of a column-major run (18 m-tiles x 2 columns at the 4608-row configs), so fewer
+// operand lines miss in that XCD's L2.
+#ifndef CKH_TILE_GROUP
+#define CKH_TILE_GROUP 6
+#endif
+constexpr int kTileGroup = CKH_TILE_GROUP;
+
+__device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, int& tm, int& tn) {
+    if (kTileGroup <= 0 || kTileGroup >= tiles_m) {
+        tm = L % tiles_m;
+        tn = L / tiles_m;
+        return;
+    }
+    const int g = L / (kTileGroup * tiles_n);
+    const int i = L - g * kTileGroup * tiles_n;
+    const int gs = min(kTileGroup, tiles_m - g * kTileGroup);  // the last group may be shorter
+    tm = g * kTileGroup + i % gs;
+    tn = i / gs;
+}
+
 }  // namespace ckh

@@ -35,8 +35,9 @@
 // c ^ ((r >> 1) & 3) ^ ((r >> 3) & 1), which makes a 32-row fragment read (one chunk
 // of 32 consecutive rows) conflict-free for both 32- and 64-bank LDS layouts.
 // Workgroups are dispatched round-robin over the 8 XCDs; the tile index is remapped
-// so each XCD walks a contiguous range of tiles (column-major over m), keeping the
-// tiles that share a weight panel on one L2.  Tiles run one per CU in rounds; when the
+// so each XCD walks a contiguous range of tiles in grouped order (grouped_tile), so the
+// tiles an XCD runs at once share few operand panels in its L2.  Tiles run one per CU
+// in rounds; when the
 // last round would be at most half full, its tiles go to a second launch as 256 x 128
 // half tiles (2 MFMA columns per wave, 8-slot stages) on twice as many CUs.
 #include <type_traits>
@@ -111,7 +112,7 @@ struct Args {
     int ncb;               // scale column blocks: ceil(K/32/4)
     int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
     int tiles_m, tiles_n;  // 256 x 256 tile grid
-    int tile_base;         // first tile of this launch (linear, column-major over m)
+    int tile_base;         // first tile of this launch (linear index, grouped order)
     int n_tiles;           // tiles in this launch (half-width launches: 2 workgroups per tile)
     // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
     const float* tsa;
@@ -297,13 +298,13 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
 
     // Workgroups are dispatched round-robin over the 8 XCDs; a full-tile launch remaps
-    // the index so each XCD walks a contiguous range of tiles (column-major over m),
-    // keeping the tiles that share a weight panel on one L2.  A half-tile launch gives
-    // tile L's two column halves to consecutive workgroups.
+    // the index so each XCD walks a contiguous range of tiles (in grouped order).  A
+    // half-tile launch gives tile L's two column halves to consecutive workgroups.
     int bid = blockIdx.x;
     if (NW == 4 && (p.n_tiles & 7) == 0) bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
     const int L = p.tile_base + (NW == 4 ? bid : bid >> 1);
-    const int tm = L % p.tiles_m, tn = L / p.tiles_m;
+    int tm, tn;
+    grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
     if (n0 >= p.N) return;  // a half tile wholly past N (uniform over the workgroup)
 

@@ -32,7 +32,7 @@
 //
 // LDS rows are 128 bytes (a group); logical 16-byte chunk c of row r is stored at
 // chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.  Workgroups
-// walk the tiles XCD-contiguously as in the MXFP8 kernel.
+// walk the tiles XCD-contiguously in grouped order, as in the MXFP8 kernel.
 #include <type_traits>
 #include <utility>
 
@@ -204,7 +204,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
     if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
-    const int tm = bid % p.tiles_m, tn = bid / p.tiles_m;
+    int tm, tn;
+    grouped_tile(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x;
