@@ -112,8 +112,8 @@ struct Args {
     int ncb;               // scale column blocks: ceil(K/32/4)
     int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
     int tiles_m, tiles_n;  // 256 x 256 tile grid
-    int tile_base;         // first tile of this launch (linear index, grouped order)
-    int n_tiles;           // tiles in this launch (half-width launches: 2 workgroups per tile)
+    int n_full;            // workgroups [0, n_full) compute full tiles 0 .. n_full-1 (linear, grouped order)
+    int n_half;            // workgroups n_full + 2 i, +1 compute the two column halves of tile n_full + i
     // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
     const float* tsa;
     const float* tsb;
@@ -285,24 +285,23 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 // E8M0 127 = 1.0) and out = tsa * tsb * (A B^T) + bias.
 // NW: 32-column MFMA tiles per wave along n: 4 for 256 x 256 workgroup tiles, 2 for the
 // 256 x 128 half tiles that finish a grid whose last round would leave most CUs idle.
+// bid: the workgroup's index among the workgroups of its kind (full or half tiles).
+//
+// Stage buffers 0, 1 and 2, 3 live in two arrays.  Every stage reads fragments from one
+// array and writes staged data into the other, so the compiler knows they never alias
+// and may interleave the two freely; within an array, per-lane addresses of different
+// buffers differ only by immediates.
 template <int OUT, int BIAS, bool UNIT, int NW>
-__global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
+__device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01, uint8_t* lds23) {
     constexpr int TBN = 64 * NW;  // tile width along n
     constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
     constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
-    // Stage buffers 0, 1 and 2, 3 in two arrays.  Every stage reads fragments from one
-    // array and writes staged data into the other, so the compiler knows they never
-    // alias and may interleave the two freely; within an array, per-lane addresses of
-    // different buffers differ only by immediates.
-    __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
 
-    // Workgroups are dispatched round-robin over the 8 XCDs; a full-tile launch remaps
-    // the index so each XCD walks a contiguous range of tiles (in grouped order).  A
-    // half-tile launch gives tile L's two column halves to consecutive workgroups.
-    int bid = blockIdx.x;
-    if (NW == 4 && (p.n_tiles & 7) == 0) bid = (bid & 7) * (p.n_tiles >> 3) + (bid >> 3);
-    const int L = p.tile_base + (NW == 4 ? bid : bid >> 1);
+    // Workgroups are dispatched round-robin over the 8 XCDs; full tiles are remapped so
+    // each XCD walks a contiguous range of tiles (in grouped order).  Half tiles give
+    // tile L's two column halves to consecutive workgroups.
+    if (NW == 4 && (p.n_full & 7) == 0) bid = (bid & 7) * (p.n_full >> 3) + (bid >> 3);
+    const int L = NW == 4 ? bid : p.n_full + (bid >> 1);
     int tm, tn;
     grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
@@ -548,6 +547,20 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     }
 }
 
+// One grid runs both kinds of workgroup: the full tiles first, then (when the last
+// round of full tiles would be at most half full) that round's tiles as half tiles.
+// The dispatcher starts half-tile workgroups on CUs as their last full tile ends, so
+// the tail overlaps the uneven end of the previous round instead of waiting for a
+// second launch.
+template <int OUT, int BIAS, bool UNIT>
+__global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
+    const int b = blockIdx.x;
+    if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4>(p, b, lds01, lds23);
+    else gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
+}
+
 }  // namespace mx
 }  // namespace ckh
 
@@ -558,9 +571,9 @@ namespace {
 // Workgroups that can hold a 256 x 256 tile at once: one per CU.
 constexpr int kGemmSlots = 256;
 
-template <bool UNIT, int NW>
-void launch_part(const mx::Args& p, unsigned wgs, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT, NW>), dim3(wgs), dim3(mx::NT), 0, st, p)
+template <bool UNIT>
+void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT>), dim3(wgs), dim3(mx::NT), 0, st, p)
 #define BY_BIAS(O)                                         \
     do {                                                   \
         if (!has_bias) LAUNCH(O, -1);                      \
@@ -576,21 +589,15 @@ void launch_part(const mx::Args& p, unsigned wgs, int out_code, int bias_code, b
 }
 
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
-// half full (e.g. 864 tiles = 3 rounds + 96), its tiles are launched separately as
-// twice as many 256 x 128 half tiles, which finish in about 55% of a full tile's time.
+// half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
+// half tiles (about 55% of a full tile's time each), in the same grid.
 template <bool UNIT>
 int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
     const int tiles = p.tiles_m * p.tiles_n;
     const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : 0;
-    const int split = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
-    p.tile_base = 0;
-    p.n_tiles = tiles - split;
-    launch_part<UNIT, 4>(p, static_cast<unsigned>(p.n_tiles), out_code, bias_code, has_bias, st);
-    if (split) {
-        p.tile_base = tiles - split;
-        p.n_tiles = split;
-        launch_part<UNIT, 2>(p, static_cast<unsigned>(2 * split), out_code, bias_code, has_bias, st);
-    }
+    p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
+    p.n_full = tiles - p.n_half;
+    launch_grid<UNIT>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
     return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }
 
