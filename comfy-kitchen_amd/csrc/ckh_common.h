@@ -220,11 +220,23 @@ __host__ __device__ __forceinline__ int64_t swz_offset(int64_t r, int64_t c, int
 // ---------------------------------------------------------- element loads
 // Streaming (nontemporal) 16-byte loads: input read once by a kernel is not kept in the
 // caches.  On gfx950 this lifts the quantizers' bandwidth by 10-15% over plain loads at
-// the benchmark sizes; nontemporal stores measured no better than plain stores.
+// the benchmark sizes.
 typedef unsigned ckh_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_stream16(const void* p) {
     ckh_u32x4 a = __builtin_nontemporal_load(static_cast<const ckh_u32x4*>(p));
     return make_uint4(a.x, a.y, a.z, a.w);
+}
+
+// Streaming (nontemporal) stores of outputs written once.  Measured against plain stores
+// on gfx950 in the benchmark runs: dequantize_per_tensor_fp8 -9%, apply_rope1 -9%,
+// apply_rope -2.5%, quantize_nvfp4 -3%, quantize_per_tensor_fp8 -1%; the MXFP8
+// quantizer's 8-byte code stores were 9% slower, so that kernel keeps plain stores.
+typedef unsigned ckh_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_stream16(void* p, uint4 v) {
+    __builtin_nontemporal_store(ckh_u32x4{v.x, v.y, v.z, v.w}, static_cast<ckh_u32x4*>(p));
+}
+__device__ __forceinline__ void st_stream8(void* p, uint2 v) {
+    __builtin_nontemporal_store(ckh_u32x2{v.x, v.y}, static_cast<ckh_u32x2*>(p));
 }
 
 // Load 8 consecutive elements of dtype code C as floats from an address aligned to

@@ -488,7 +488,7 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
                     nvfp4_codes8_div_rare<HI_FIRST>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15], T));
             }
         }
-        if (r[u] < rows && j[u] < n_cb) *reinterpret_cast<uint2*>(qx + off[u] / 2) = codes;
+        if (r[u] < rows && j[u] < n_cb) st_stream8(qx + off[u] / 2, codes);
         uint32_t word = s8 << (8 * l);
         word |= dpp<0xB1>(word);  // quad_perm [1,0,3,2]
         word |= dpp<0x4E>(word);  // quad_perm [2,3,0,1]
@@ -500,7 +500,7 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         const uint32_t jj = threadIdx.x >> 3, part = threadIdx.x & 7, jc = it.cg * G + jj;
         if (jc < n_cb) {
             const uint4 v = *reinterpret_cast<const uint4*>(&sw[jj][part * 4]);
-            *reinterpret_cast<uint4*>(sc + (it.tile * n_cb + jc) * 128 + it.q * 32 + part * 4) = v;
+            st_stream16(sc + (it.tile * n_cb + jc) * 128 + it.q * 32 + part * 4, v);
         }
     }
 }

@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
                 w[q] = acc;
             }
         }
-        *reinterpret_cast<uint4*>(out + i0) = make_uint4(w[0], w[1], w[2], w[3]);
+        st_stream16(out + i0, make_uint4(w[0], w[1], w[2], w[3]));
     } else {
         for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i)
             out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
@@ -90,9 +90,10 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
 template <int OUT>
 __device__ __forceinline__ void store16_hw(void* out, int64_t i, const float (&v)[16]) {
     if constexpr (OUT == CKH_F32) {
-        float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+        float* p = static_cast<float*>(out) + i;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        for (int q = 0; q < 4; ++q)
+            st_stream16(p + 4 * q, make_uint4(as_u(v[4 * q]), as_u(v[4 * q + 1]), as_u(v[4 * q + 2]), as_u(v[4 * q + 3])));
     } else {
         uint32_t w[8];
 #pragma unroll
@@ -101,9 +102,9 @@ __device__ __forceinline__ void store16_hw(void* out, int64_t i, const float (&v
             uint32_t hi = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
             w[q] = lo | (hi << 16);
         }
-        uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i);
-        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+        uint16_t* p = static_cast<uint16_t*>(out) + i;
+        st_stream16(p, make_uint4(w[0], w[1], w[2], w[3]));
+        st_stream16(p + 8, make_uint4(w[4], w[5], w[6], w[7]));
     }
 }
 

@@ -235,8 +235,8 @@ __global__ __launch_bounds__(256) void rope_wave_kernel(RopeWaveArgs a) {
             nq = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
             if (a.xk) nk = ld_stream16(static_cast<const uint16_t*>(a.xk) + xo);
         }
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.oq) + o_cur) = rotate8<XC, FC>(cq, f);
-        if (a.xk) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.ok) + o_cur) = rotate8<XC, FC>(ck, f);
+        st_stream16(static_cast<uint16_t*>(a.oq) + o_cur, rotate8<XC, FC>(cq, f));
+        if (a.xk) st_stream16(static_cast<uint16_t*>(a.ok) + o_cur, rotate8<XC, FC>(ck, f));
         cq = nq;
         ck = nk;
     }
