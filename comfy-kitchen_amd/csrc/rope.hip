@@ -126,7 +126,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
 // A wave holds W = 64/L consecutive freqs rows p; the workgroup's four waves share
 // them and take every fourth x row rho of the rows that broadcast over them (the same
 // freqs), so each lane loads its four rotation matrices once and then streams up to
-// kRowsPerWave rows of q and of k, loading row i+1 while row i is rotated and stored.  With Flux's layout (freqs over the sequence,
+// kRowsPerWave rows of q and of k, loading row i+1 while row i is rotated and stored
+// (apply_rope1: all rows loaded first).  With Flux's layout (freqs over the sequence,
 // broadcast over heads) consecutive p are consecutive x rows, so every load
 // instruction reads W * head_dim * 2 contiguous bytes.  The rho -> (b, d1, d2)
 // decomposition is wave-uniform and done in scalar registers.
@@ -178,7 +179,8 @@ __device__ __forceinline__ uint4 rotate8(uint4 w, const float (&f)[4][4]) {
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-template <int XC, int FC>
+// ONE: apply_rope1 (no k tensor)
+template <int XC, int FC, bool ONE>
 __global__ __launch_bounds__(256) void rope_wave_kernel(RopeWaveArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -212,33 +214,57 @@ __global__ __launch_bounds__(256) void rope_wave_kernel(RopeWaveArgs a) {
 
     const int r0 = blockIdx.y * a.rows_per_block + wave;
     const int r_end = min(a.R, static_cast<int>(blockIdx.y + 1) * a.rows_per_block);
-    // software pipeline: row i+1's loads are in flight while row i is rotated and stored
-    auto offs = [&](int rho, int64_t& xo, int64_t& oo) {
-        const int r2 = rho % a.R2, r1 = (rho / a.R2) % a.R1, rb = rho / (a.R2 * a.R1);
-        xo = xbase + rb * a.sxb + r1 * a.sx1 + r2 * a.sx2;
-        oo = obase + ((rb * a.D1 + r1) * a.D2 + r2) * a.hd;
-    };
-    int64_t xo, oo;
-    uint4 cq = make_uint4(0, 0, 0, 0), ck = cq;
-    if (r0 < r_end) {
-        offs(r0, xo, oo);
-        cq = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
-        if (a.xk) ck = ld_stream16(static_cast<const uint16_t*>(a.xk) + xo);
-    }
+    if constexpr (ONE) {
+        // apply_rope1: all of the wave's rows are loaded before any is rotated (up to
+        // kRowsPerWave 16-byte loads in flight per lane); measured 3.5% faster than the
+        // pipelined loop below for q alone, 2% slower for q and k
+        int64_t oo[kRowsPerWave];
+        uint4 cq[kRowsPerWave];
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i) {
-        if (r0 + 4 * i >= r_end) break;
-        const int64_t o_cur = oo;
-        uint4 nq = cq, nk = ck;
-        if (i + 1 < kRowsPerWave && r0 + 4 * (i + 1) < r_end) {
-            offs(r0 + 4 * (i + 1), xo, oo);
-            nq = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
-            if (a.xk) nk = ld_stream16(static_cast<const uint16_t*>(a.xk) + xo);
+        for (int i = 0; i < kRowsPerWave; ++i) {
+            const int rho = r0 + 4 * i;
+            if (rho < r_end) {
+                const int r2 = rho % a.R2, r1 = (rho / a.R2) % a.R1, rb = rho / (a.R2 * a.R1);
+                const int64_t xo = xbase + rb * a.sxb + r1 * a.sx1 + r2 * a.sx2;
+                oo[i] = obase + ((rb * a.D1 + r1) * a.D2 + r2) * a.hd;
+                cq[i] = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
+            }
         }
-        st_stream16(static_cast<uint16_t*>(a.oq) + o_cur, rotate8<XC, FC>(cq, f));
-        if (a.xk) st_stream16(static_cast<uint16_t*>(a.ok) + o_cur, rotate8<XC, FC>(ck, f));
-        cq = nq;
-        ck = nk;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave; ++i) {
+            if (r0 + 4 * i >= r_end) break;
+            st_stream16(static_cast<uint16_t*>(a.oq) + oo[i], rotate8<XC, FC>(cq[i], f));
+        }
+    } else {
+        // apply_rope: software pipeline, row i+1's loads in flight while row i is rotated
+        // and stored
+        auto offs = [&](int rho, int64_t& xo, int64_t& oo) {
+            const int r2 = rho % a.R2, r1 = (rho / a.R2) % a.R1, rb = rho / (a.R2 * a.R1);
+            xo = xbase + rb * a.sxb + r1 * a.sx1 + r2 * a.sx2;
+            oo = obase + ((rb * a.D1 + r1) * a.D2 + r2) * a.hd;
+        };
+        int64_t xo, oo;
+        uint4 cq = make_uint4(0, 0, 0, 0), ck = cq;
+        if (r0 < r_end) {
+            offs(r0, xo, oo);
+            cq = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
+            if (a.xk) ck = ld_stream16(static_cast<const uint16_t*>(a.xk) + xo);
+        }
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave; ++i) {
+            if (r0 + 4 * i >= r_end) break;
+            const int64_t o_cur = oo;
+            uint4 nq = cq, nk = ck;
+            if (i + 1 < kRowsPerWave && r0 + 4 * (i + 1) < r_end) {
+                offs(r0 + 4 * (i + 1), xo, oo);
+                nq = ld_stream16(static_cast<const uint16_t*>(a.xq) + xo);
+                if (a.xk) nk = ld_stream16(static_cast<const uint16_t*>(a.xk) + xo);
+            }
+            st_stream16(static_cast<uint16_t*>(a.oq) + o_cur, rotate8<XC, FC>(cq, f));
+            if (a.xk) st_stream16(static_cast<uint16_t*>(a.ok) + o_cur, rotate8<XC, FC>(ck, f));
+            cq = nq;
+            ck = nk;
+        }
     }
 }
 
@@ -302,7 +328,11 @@ extern "C" int ckh_apply_rope(const void* xq, const void* xk, const void* freqs,
         w.rows_per_block = static_cast<int32_t>(rup(cdiv(a.R, chunks), 4));  // <= 4 * kRowsPerWave
         CKH_REQUIRE(chunks < 65536, "apply_rope: grid too large");
         dim3 grid(static_cast<unsigned>(cdiv(P, 64 / lanes)), static_cast<unsigned>(chunks));
-#define LAUNCH_W(XC, FC) hipLaunchKernelGGL((rope_wave_kernel<XC, FC>), grid, dim3(256), 0, st, w)
+#define LAUNCH_W(XC, FC)                                                                        \
+    do {                                                                                        \
+        if (xk) hipLaunchKernelGGL((rope_wave_kernel<XC, FC, false>), grid, dim3(256), 0, st, w); \
+        else hipLaunchKernelGGL((rope_wave_kernel<XC, FC, true>), grid, dim3(256), 0, st, w);    \
+    } while (0)
 #define BY_FC_W(XC)                                         \
     do {                                                    \
         if (freqs_code == CKH_F32) LAUNCH_W(XC, CKH_F32);       \
