@@ -456,36 +456,52 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
-        float c;
-        if (g_ok && amax >= 0x1p-60f && amax <= 0x1p60f) {
-            const float c0 = amax * y6;
-            const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
-            const float d0 = c1 * yg;
-            c = __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
-        } else {
-            c = nvfp4_c_div_rare(amax, g);
-        }
-        const uint32_t s8 = r[u] < rows ? nvfp4_scale_code_of(c, amax, g) : 0u;
-        const float T = nvfp4_total(g, s8);
+        // the scale by the exact steps (valid when g and amax are within [2^-60, 2^60])
+        const float c0 = amax * y6;
+        const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
+        const float d0 = c1 * yg;
+        const float cf = __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
+        const uint32_t s8f = hw_e4m3x4(cf, 0.0f, 0.0f, 0.0f) & 0xffu;
         float v[16];
         unpack16x8<IN>(w[u][0], *reinterpret_cast<float(*)[8]>(&v[0]));
         unpack16x8<IN>(w[u][1], *reinterpret_cast<float(*)[8]>(&v[8]));
+        uint32_t s8;
         uint2 codes = make_uint2(0u, 0u);
-        if (T != 0.0f) {
-            if (c <= 448.0f && T >= 0x1p-120f && T <= 0x1p120f) {
-                const float y = 1.0f / T;
-                float q[16];
+        // Common blocks: 0 < c <= 448 and s8 != 0, so s8 is the convert of c (no clamp,
+        // no NaN), T = g * s8 lies in [2^-69, 2^69] and the exact division steps apply.
+        // A row past the end has amax 0 and takes the general path.
+        if (g_ok && amax >= 0x1p-60f && amax <= 0x1p60f && cf <= 448.0f && s8f != 0u) {
+            s8 = s8f;
+            const float T = g * hw_e4m3_to_f<0>(s8f);
+            const float y = 1.0f / T;
+            float q[16];
 #pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    const float q0 = v[t] * y;
-                    const float e = __builtin_fmaf(T, q0, -v[t]);
-                    q[t] = __builtin_fmaf(-e, y, q0);
+            for (int t = 0; t < 16; ++t) {
+                const float q0 = v[t] * y;
+                const float e = __builtin_fmaf(T, q0, -v[t]);
+                q[t] = __builtin_fmaf(-e, y, q0);
+            }
+            codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+        } else {
+            const float c = g_ok && amax >= 0x1p-60f && amax <= 0x1p60f ? cf : nvfp4_c_div_rare(amax, g);
+            s8 = r[u] < rows ? nvfp4_scale_code_of(c, amax, g) : 0u;
+            const float T = nvfp4_total(g, s8);
+            if (T != 0.0f) {
+                if (c <= 448.0f && T >= 0x1p-120f && T <= 0x1p120f) {
+                    const float y = 1.0f / T;
+                    float q[16];
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) {
+                        const float q0 = v[t] * y;
+                        const float e = __builtin_fmaf(T, q0, -v[t]);
+                        q[t] = __builtin_fmaf(-e, y, q0);
+                    }
+                    codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+                } else {
+                    codes = make_uint2(
+                        nvfp4_codes8_div_rare<HI_FIRST>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], T),
+                        nvfp4_codes8_div_rare<HI_FIRST>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15], T));
                 }
-                codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
-            } else {
-                codes = make_uint2(
-                    nvfp4_codes8_div_rare<HI_FIRST>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], T),
-                    nvfp4_codes8_div_rare<HI_FIRST>(v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15], T));
             }
         }
         if (r[u] < rows && j[u] < n_cb) st_stream8(qx + off[u] / 2, codes);
