@@ -432,20 +432,20 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     constexpr uint32_t kUnitsPerPass = 16 * G;
     const FastItem it = fast_item(n_items, n_cg, cg_magic, cg_shift);
     if (!it.valid) return;
-    __shared__ uint32_t sw[G][32];
+    __shared__ uint32_t sw[G * 32];
     const uint32_t l = threadIdx.x & 3;
     const float g = gptr[0];
     const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
     const float yg = 1.0f / g;
     constexpr float y6 = 1.0f / 6.0f;
     uint4 w[kNvUnits][2];
-    uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits];
+    uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
-        const uint32_t ul = u * kUnitsPerPass + (threadIdx.x >> 2);  // unit in the workgroup
-        const uint32_t rs = ul / G;                                  // row slot: 8 rows x 4 groups
+        ul[u] = u * kUnitsPerPass + (threadIdx.x >> 2);  // unit in the workgroup
+        const uint32_t rs = ul[u] / G;                   // row slot: 8 rows x 4 groups
         r[u] = it.tile * 128 + (rs & 3) * 32 + it.q * 8 + (rs >> 2);
-        j[u] = it.cg * G + ul % G;
+        j[u] = it.cg * G + ul[u] % G;
         off[u] = r[u] * cols + 64 * j[u] + 16 * l;
         w[u][0] = w[u][1] = make_uint4(0u, 0u, 0u, 0u);
         if (r[u] < rows && j[u] < n_cb) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
         const float d0 = c1 * yg;
         const float cf = __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
-        const uint32_t s8f = hw_e4m3x4(cf, 0.0f, 0.0f, 0.0f) & 0xffu;
+        const uint32_t s8f = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(cf, 0.0f, 0, false)) & 0xffu;
         float v[16];
         unpack16x8<IN>(w[u][0], *reinterpret_cast<float(*)[8]>(&v[0]));
         unpack16x8<IN>(w[u][1], *reinterpret_cast<float(*)[8]>(&v[8]));
@@ -508,14 +508,16 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         uint32_t word = s8 << (8 * l);
         word |= dpp<0xB1>(word);  // quad_perm [1,0,3,2]
         word |= dpp<0x4E>(word);  // quad_perm [2,3,0,1]
-        // word (r, j) sits at ((tile*n_cb + j)*32 + (r & 31))*4 + (r & 127)/32
-        if (l == 0) sw[j[u] % G][((r[u] & 31) - it.q * 8) * 4 + ((r[u] & 127) >> 5)] = word;
+        // Word (r, j) of the tensor sits at ((tile*n_cb + j)*32 + (r & 31))*4 + (r & 127)/32.
+        // The workgroup stages the words of unit column j % G as one 32-word line, in which
+        // row r is word ((r & 31) - 8 q) * 4 + (r & 127) / 32, i.e. its row slot ul / G.
+        if (l == 0) sw[(ul[u] % G) * 32 + ul[u] / G] = word;
     }
     __syncthreads();
     if (threadIdx.x < 8 * G) {
         const uint32_t jj = threadIdx.x >> 3, part = threadIdx.x & 7, jc = it.cg * G + jj;
         if (jc < n_cb) {
-            const uint4 v = *reinterpret_cast<const uint4*>(&sw[jj][part * 4]);
+            const uint4 v = *reinterpret_cast<const uint4*>(&sw[jj * 32 + part * 4]);
             st_stream16(sc + (it.tile * n_cb + jc) * 128 + it.q * 32 + part * 4, v);
         }
     }
