@@ -488,7 +488,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the quantizers/GEMMs shard by rows with no exchange; see DESIGN.md).", file=sys.stderr)
+              "(the quantizers and GEMMs would shard by rows with no exchange between GPUs).", file=sys.stderr)
         sys.exit(2)
     configs = set(args.configs.split(","))
 
