@@ -57,9 +57,11 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_scaled_mm_mxfp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_fp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
-    "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
+    "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _p, _u64]),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
+# CKH_AMAX_WORKSPACE_BYTES of include/ckh.h: the workspace ckh_amax_scale takes
+AMAX_WORKSPACE_BYTES = 8192
 
 _lib: ctypes.CDLL | None = None
 
@@ -162,9 +164,11 @@ def amax_scale(x: torch.Tensor, divisor: float) -> torch.Tensor:
     if x.numel() == 0:
         raise RuntimeError("amax_scale: empty tensor")
     out = torch.empty((), dtype=torch.float32, device=x.device)
+    # per-workgroup partial maxima (CKH_AMAX_WORKSPACE_BYTES), from torch's allocator
+    work = torch.empty(AMAX_WORKSPACE_BYTES // 4, dtype=torch.int32, device=x.device)
     with _on_device(x):
         _call("ckh_amax_scale", x.data_ptr(), x.numel(), DTYPE_TO_CODE[x.dtype], float(divisor), out.data_ptr(),
-              _stream(x))
+              work.data_ptr(), _stream(x))
     return out
 
 

@@ -4,23 +4,25 @@
 // tensor/nvfp4.py:64-69: ... / (448 * 6)): a 0-dim tensor of x's dtype, i.e. the fp32
 // quotient of the (exact) amax and the divisor rounded once to x's dtype.
 //
-// Three launches on the caller's stream, no allocation and no host synchronisation, so
+// Two launches on the caller's stream, no allocation and no host synchronisation, so
 // the scale feeds the quantize kernels (which read it from device memory) directly:
-//   1. clear the 4-byte result word (a kernel, so the sequence can be graph-captured);
-//   2. the maximum of |x| as ordered integer bits (NaN orders above inf, so a NaN
-//      propagates as in torch.amax) with one atomic max per workgroup into that word;
-//   3. divide by `divisor`, round to x's dtype and store the fp32 value in place.
-// Pass 2 reads x with ordinary (cached) loads: the quantize kernel that follows finds
-// the tensor in the 256 MB infinity cache when it fits there.
+//   1. each workgroup writes the maximum of |x| over its share, as ordered integer bits
+//      (NaN orders above inf, so a NaN propagates as in torch.amax), to its word of the
+//      caller's workspace;
+//   2. one workgroup reduces those words, divides by `divisor`, rounds to x's dtype and
+//      stores the fp32 value.
+// No atomics and no cleared words: every workspace word that pass 2 reads was written by
+// pass 1 of the same call.  Pass 1 reads x with ordinary (cached) loads, kUnroll 16-byte
+// loads in flight per thread: the quantize kernel that follows finds the tensor in the
+// 256 MB infinity cache when it fits there.
 #include "ckh_common.h"
 
 namespace ckh {
 namespace am {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;  // 16-byte loads in flight per thread per iteration
-
-__global__ void clear_kernel(uint32_t* word) { *word = 0u; }
+constexpr int kUnroll = 16;                // 16-byte loads in flight per thread
+constexpr int kMaxBlocks = CKH_AMAX_WORKSPACE_BYTES / 4;  // one partial word per workgroup
 
 // |x| bits of 8 packed 16-bit values -> the largest, as fp32 bits
 template <int IN>
@@ -44,9 +46,32 @@ __device__ __forceinline__ uint32_t abs_bits1(const void* x, int64_t i) {
     else return to_f32_bits<IN>(static_cast<const uint16_t*>(x)[i] & 0x7fffu);
 }
 
-// VEC: x is 16-byte aligned; chunks of 16 bytes, then a scalar tail.
+template <int IN>
+__device__ __forceinline__ uint32_t chunk_max(uint4 w) {
+    if constexpr (IN == CKH_F32)
+        return max(max(w.x & 0x7fffffffu, w.y & 0x7fffffffu), max(w.z & 0x7fffffffu, w.w & 0x7fffffffu));
+    else return to_f32_bits<IN>(max16<IN>(w));
+}
+
+// the workgroup's maximum of m (every thread must call it); valid in thread 0
+__device__ __forceinline__ uint32_t block_max(uint32_t m) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, 64)));
+    __shared__ uint32_t wmax[kThreads / 64];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    uint32_t b = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) b = max(b, wmax[w]);
+    return b;
+}
+
+// VEC: x is 16-byte aligned; chunks of 16 bytes, then a scalar tail.  Thread t reads
+// chunks t, t + stride, ... in batches of kUnroll, all of a batch's loads issued before
+// any is used.
 template <int IN, bool VEC>
-__global__ __launch_bounds__(kThreads) void amax_kernel(const void* __restrict__ x, int64_t n, uint32_t* word) {
+__global__ __launch_bounds__(kThreads) void amax_kernel(const void* __restrict__ x, int64_t n,
+                                                        uint32_t* __restrict__ partial) {
     constexpr int PER = 16 / ElemSize<IN>::value;  // elements per 16-byte chunk
     const int64_t tid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
@@ -55,54 +80,38 @@ __global__ __launch_bounds__(kThreads) void amax_kernel(const void* __restrict__
     if constexpr (VEC) {
         const int64_t chunks = n / PER;
         const uint4* p = static_cast<const uint4*>(x);
-        int64_t c = tid;
-        for (; c + (kUnroll - 1) * stride < chunks; c += kUnroll * stride) {
+        for (int64_t c0 = tid; c0 < chunks; c0 += kUnroll * stride) {
             uint4 w[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) w[u] = p[c + u * stride];
-#pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
-                if constexpr (IN == CKH_F32)
-                    m = max(m, max(max(w[u].x & 0x7fffffffu, w[u].y & 0x7fffffffu),
-                                   max(w[u].z & 0x7fffffffu, w[u].w & 0x7fffffffu)));
-                else
-                    m = max(m, to_f32_bits<IN>(max16<IN>(w[u])));
+                const int64_t c = c0 + u * stride;
+                w[u] = c < chunks ? p[c] : make_uint4(0u, 0u, 0u, 0u);
             }
-        }
-        for (; c < chunks; c += stride) {
-            const uint4 w = p[c];
-            if constexpr (IN == CKH_F32)
-                m = max(m, max(max(w.x & 0x7fffffffu, w.y & 0x7fffffffu), max(w.z & 0x7fffffffu, w.w & 0x7fffffffu)));
-            else
-                m = max(m, to_f32_bits<IN>(max16<IN>(w)));
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) m = max(m, chunk_max<IN>(w[u]));
         }
         tail_begin = chunks * PER;
     }
     for (int64_t i = tail_begin + tid; i < n; i += stride) m = max(m, abs_bits1<IN>(x, i));
-    // wave maximum, then the workgroup's through LDS, then one atomic per workgroup (a
-    // vector-memory atomic; same-address atomics serialise, so there are few of them)
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, 64)));
-    __shared__ uint32_t wmax[kThreads / 64];
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t b = wmax[0];
-#pragma unroll
-        for (int w = 1; w < kThreads / 64; ++w) b = max(b, wmax[w]);
-        atomicMax(word, b);
-    }
+    const uint32_t b = block_max(m);
+    if (threadIdx.x == 0) partial[blockIdx.x] = b;
 }
 
-// word holds the amax as fp32 bits; replace it with float(round_IN(amax / divisor))
+// *out = float(round_IN(amax / divisor)), amax = the largest of the nblocks partial words
 template <int IN>
-__global__ void finalize_kernel(uint32_t* word, float divisor) {
-    const float q = as_f(*word) / divisor;
-    float r;
-    if constexpr (IN == CKH_BF16) r = bf16_to_f(f_to_bf16(q));
-    else if constexpr (IN == CKH_F16) r = round_f16(q);
-    else r = q;
-    *reinterpret_cast<float*>(word) = r;
+__global__ __launch_bounds__(kThreads) void finalize_kernel(const uint32_t* __restrict__ partial, int nblocks,
+                                                            float divisor, float* __restrict__ out) {
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < nblocks; i += kThreads) m = max(m, partial[i]);
+    const uint32_t b = block_max(m);
+    if (threadIdx.x == 0) {
+        const float q = as_f(b) / divisor;
+        float r;
+        if constexpr (IN == CKH_BF16) r = bf16_to_f(f_to_bf16(q));
+        else if constexpr (IN == CKH_F16) r = round_f16(q);
+        else r = q;
+        *out = r;
+    }
 }
 
 }  // namespace am
@@ -111,27 +120,26 @@ __global__ void finalize_kernel(uint32_t* word, float divisor) {
 using namespace ckh;
 
 extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
-                              uintptr_t stream) {
-    CKH_REQUIRE(x && scale_out, "amax_scale: null pointer");
+                              void* workspace, uintptr_t stream) {
+    CKH_REQUIRE(x && scale_out && workspace, "amax_scale: null pointer");
     CKH_REQUIRE(numel > 0, "amax_scale: empty tensor (torch.amax of an empty tensor is an error too)");
     CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
                 "amax_scale: unsupported input dtype code %d", in_code);
-    CKH_REQUIRE(aligned(scale_out, 4), "amax_scale: output misaligned");
+    CKH_REQUIRE(aligned(scale_out, 4) && aligned(workspace, 4), "amax_scale: output or workspace misaligned");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    uint32_t* word = static_cast<uint32_t*>(scale_out);
+    uint32_t* partial = static_cast<uint32_t*>(workspace);
     const int es = in_code == CKH_F32 ? 4 : 2;
     const bool vec = aligned(x, 16);
-    // four workgroups per CU at most (1024 atomics); each thread strides through x with
-    // kUnroll 16-byte loads in flight
+    // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight
     const int64_t chunks = cdiv(numel * es, 16);
-    const unsigned blocks =
-        static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(1024, cdiv(chunks, am::kThreads * am::kUnroll))));
-    hipLaunchKernelGGL(am::clear_kernel, dim3(1), dim3(1), 0, st, word);
-#define LAUNCH(I)                                                                                      \
-    do {                                                                                               \
-        if (vec) hipLaunchKernelGGL((am::amax_kernel<I, true>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, word); \
-        else hipLaunchKernelGGL((am::amax_kernel<I, false>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, word); \
-        hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(1), 0, st, word, divisor);           \
+    const int blocks = static_cast<int>(
+        std::max<int64_t>(1, std::min<int64_t>(am::kMaxBlocks, cdiv(chunks, am::kThreads * am::kUnroll))));
+#define LAUNCH(I)                                                                                            \
+    do {                                                                                                     \
+        if (vec) hipLaunchKernelGGL((am::amax_kernel<I, true>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
+        else hipLaunchKernelGGL((am::amax_kernel<I, false>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
+        hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(am::kThreads), 0, st, partial, blocks, divisor, \
+                           static_cast<float*>(scale_out));                                                  \
     } while (0)
     if (in_code == CKH_F32) LAUNCH(CKH_F32);
     else if (in_code == CKH_F16) LAUNCH(CKH_F16);

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 2
+#define CKH_ABI_VERSION 3
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -171,14 +171,17 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
  * Dynamic per-tensor scale: *scale_out = float(round_x(amax(|x|) / divisor)), the amax
  * and the quotient rounded to x's dtype (in_code), as the layouts' default scale
  * torch.amax(tensor.abs()) / max computes it.  x: numel contiguous elements; scale_out:
- * one f32 on device, used as the reduction's scratch word, so no allocation.  A NaN in
- * x gives a NaN scale.  Replaces that torch expression in TensorCoreFP8Layout.quantize
- * (tensor/fp8.py:56-61, divisor 448) and TensorCoreNVFP4Layout.quantize
- * (tensor/nvfp4.py:64-69, divisor 2688); the result feeds ckh_quantize_fp8 /
- * ckh_quantize_nvfp4 on the same stream without a host round trip.
+ * one f32 on device; workspace: CKH_AMAX_WORKSPACE_BYTES of device memory (4-byte
+ * aligned, contents ignored and overwritten) that holds the per-workgroup partial maxima,
+ * so the call allocates nothing.  Calls running at the same time need workspaces of their
+ * own.  A NaN in x gives a NaN scale.  Replaces that torch expression in
+ * TensorCoreFP8Layout.quantize (tensor/fp8.py:56-61, divisor 448) and
+ * TensorCoreNVFP4Layout.quantize (tensor/nvfp4.py:64-69, divisor 2688); the result feeds
+ * ckh_quantize_fp8 / ckh_quantize_nvfp4 on the same stream without a host round trip.
  */
+#define CKH_AMAX_WORKSPACE_BYTES 8192
 int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
-                   uintptr_t stream);
+                   void* workspace, uintptr_t stream);
 
 #ifdef __cplusplus
 }

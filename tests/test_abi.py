@@ -32,7 +32,12 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 2
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 3
+
+
+def test_amax_workspace_size_matches_header():
+    m = re.search(r"#define CKH_AMAX_WORKSPACE_BYTES (\d+)", HEADER.read_text())
+    assert m and int(m.group(1)) == hb.AMAX_WORKSPACE_BYTES
 
 
 def test_invalid_arguments_return_error(lib):
@@ -48,6 +53,14 @@ def test_invalid_arguments_return_error(lib):
     assert b"xk and xk_out" in lib.ckh_last_error()
     assert lib.ckh_apply_rope(p, None, p, p, None, 1, 2, 3, 128, 1, 5, 3, 0, 0, 0, 0, 0, 0, 2, 0, 0) == 1
     assert b"does not broadcast" in lib.ckh_last_error()
+    f = lib.ckh_amax_scale
+    f.argtypes = hb.SIGNATURES["ckh_amax_scale"][1]
+    assert f(p, 16, 2, 448.0, p, None, 0) == 1  # no workspace
+    assert b"null pointer" in lib.ckh_last_error()
+    assert f(p, 16, 2, 448.0, p, p + 2, 0) == 1
+    assert b"misaligned" in lib.ckh_last_error()
+    assert f(p, 0, 2, 448.0, p, p, 0) == 1
+    assert b"empty tensor" in lib.ckh_last_error()
 
 
 def test_zero_sized_calls_are_noops(lib):

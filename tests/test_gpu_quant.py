@@ -287,6 +287,19 @@ def test_amax_scale_matches_torch(dtype, n, divisor, hip, seed):
     assert torch.equal(got.cpu().view(torch.int32), want.view(torch.int32))
 
 
+@pytest.mark.parametrize("n", [8192 * 5120, 8192 * 5120 + 5])
+def test_amax_scale_full_grid(n, hip, seed):
+    # enough chunks for every workgroup of the partial pass to run two batches; the
+    # largest magnitude sits in the last 16-byte chunk, or in the scalar tail
+    x = torch.randn(n).bfloat16()
+    x[n - 1] = -977.0
+    want = ref.default_scale(x, 2688.0)
+    assert torch.equal(ck.amax_scale(x.cuda(), 2688.0).cpu(), want)
+    x[n - 1] = 0.5
+    x[n // 3] = 611.0
+    assert torch.equal(ck.amax_scale(x.cuda(), 2688.0).cpu(), ref.default_scale(x, 2688.0))
+
+
 def test_amax_scale_misaligned_nan_and_sign(hip, seed):
     x = torch.randn(4099).bfloat16()
     x[1000] = -1234.5  # the amax is taken of |x|
