@@ -412,6 +412,20 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 // for the codes c <= 448 (so |v/T| < 10) and T within [2^-120, 2^120]; other blocks use
 // the IEEE divisions.  The E2M1 convert saturates out-of-range inputs to +-6 exactly as
 // the reference's clamp (checked on all 2^32 non-NaN floats), so no clamp is needed.
+// Codes of a 16-element block by the exact division steps above (the guards hold).
+template <bool HI_FIRST>
+__device__ __forceinline__ uint2 nvfp4_codes16_exact(const float (&v)[16], float T) {
+    const float y = 1.0f / T;
+    float q[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const float q0 = v[t] * y;
+        const float e = __builtin_fmaf(T, q0, -v[t]);
+        q[t] = __builtin_fmaf(-e, y, q0);
+    }
+    return make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+}
+
 constexpr int kNvUnits = 2;  // units per thread: 2 passes cover a workgroup's 32 rows x G units
 
 // G = unit columns per item (4 or 16); the workgroup has 64*G threads.  A wave's 16
@@ -472,31 +486,14 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         // A row past the end has amax 0 and takes the general path.
         if (g_ok && amax >= 0x1p-60f && amax <= 0x1p60f && cf <= 448.0f && s8f != 0u) {
             s8 = s8f;
-            const float T = g * hw_e4m3_to_f<0>(s8f);
-            const float y = 1.0f / T;
-            float q[16];
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const float q0 = v[t] * y;
-                const float e = __builtin_fmaf(T, q0, -v[t]);
-                q[t] = __builtin_fmaf(-e, y, q0);
-            }
-            codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+            codes = nvfp4_codes16_exact<HI_FIRST>(v, g * hw_e4m3_to_f<0>(s8f));
         } else {
             const float c = g_ok && amax >= 0x1p-60f && amax <= 0x1p60f ? cf : nvfp4_c_div_rare(amax, g);
             s8 = r[u] < rows ? nvfp4_scale_code_of(c, amax, g) : 0u;
             const float T = nvfp4_total(g, s8);
             if (T != 0.0f) {
                 if (c <= 448.0f && T >= 0x1p-120f && T <= 0x1p120f) {
-                    const float y = 1.0f / T;
-                    float q[16];
-#pragma unroll
-                    for (int t = 0; t < 16; ++t) {
-                        const float q0 = v[t] * y;
-                        const float e = __builtin_fmaf(T, q0, -v[t]);
-                        q[t] = __builtin_fmaf(-e, y, q0);
-                    }
-                    codes = make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+                    codes = nvfp4_codes16_exact<HI_FIRST>(v, T);
                 } else {
                     codes = make_uint2(
                         nvfp4_codes8_div_rare<HI_FIRST>(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], T),
