@@ -4,7 +4,6 @@ Markers: `gpu` tests need an MI355X (gfx950) and the built libckh.so; everything
 runs on the CPU.  The product package lives in comfy-kitchen_amd/ and is imported as
 `comfy_kitchen`; the CPU oracle (test infrastructure) is the top-level `oracle` package.
 """
-import os
 import sys
 from pathlib import Path
 
