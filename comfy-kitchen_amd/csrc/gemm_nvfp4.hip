@@ -7,7 +7,7 @@
 // (tensor_scale_a * tensor_scale_b).
 //
 // Arithmetic.  The gfx950 block-scaled MFMAs take only power-of-two (E8M0) scales, and
-// E2M1 * E4M3 needs up to 5 significant bits, so no FP8/FP6/FP4 element format holds
+// E2M1 * E4M3 needs up to 6 significant bits, so no FP8/FP6/FP4 element format holds
 // the scaled values exactly.  Each E2M1 code times its E4M3 block scale is an exact
 // fp16 (magnitudes in [2^-10, 2688]), so the operands are decoded to fp16 in registers
 // (v_cvt_scalef32_pk_f16_fp4 with scale 1, then a packed multiply by the block scale,
