@@ -6,8 +6,10 @@ Workloads are BASELINE.json's five configs, on seeded synthetic inputs:
   c1  quantize_per_tensor_fp8 + dequantize_per_tensor_fp8, bf16 [4096, 3072]
   c2  apply_rope (q, k) and apply_rope1 (q), bf16 [1, 24, 4608, 128], Flux freqs
   c3  quantize_mxfp8, bf16 [4608, 3072] with per-row log-normal magnitudes   <- `value`
+      (+ dequantize_mxfp8 of the result, bf16 out)
   c4  scaled_mm_mxfp8, [4608, 3072] x [12288, 3072] -> bf16
-  c5  quantize_nvfp4 [8192, 5120] + scaled_mm_nvfp4 [8192, 5120] x [13824, 5120]
+  c5  quantize_nvfp4 [8192, 5120] (+ dequantize_nvfp4 of the result)
+      + scaled_mm_nvfp4 [8192, 5120] x [13824, 5120]
 
 Timing: W untimed warmup steps, then K steps captured in one HIP graph and replayed
 between HIP events on the launch stream (torch's current stream, where the ops
@@ -108,7 +110,9 @@ BYTES = {
     "apply_rope": 4 * 24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4,
     "apply_rope1": 2 * 24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4,
     "quantize_mxfp8": 4608 * 3072 * 3 + 4608 * 96,
+    "dequantize_mxfp8": 4608 * 3072 * 3 + 4608 * 96,
     "quantize_nvfp4": 8192 * 5120 * 2 + 8192 * 2560 + 8192 * 320 + 4,
+    "dequantize_nvfp4": 8192 * 5120 * 2 + 8192 * 2560 + 8192 * 320 + 4,
 }
 FLOPS = {
     "scaled_mm_mxfp8": 2 * 4608 * 12288 * 3072,
@@ -259,6 +263,17 @@ def run_gpu(configs, steps, warmup, log):
                                                                  traffic.get("quantize_mxfp8"))}
             log(f"c3 quantize_mxfp8: {ms * 1e3:.2f} us")
             del xs
+            # the layouts' dequantize of the same tensor (bf16 out)
+            want = ck.dequantize_mxfp8(qa, sa)
+            nset = _sets_for(BYTES["dequantize_mxfp8"])
+            qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
+            ms = time_graph(lambda i: (lambda: ck.dequantize_mxfp8(*qs_[i])), nset, steps, warmup,
+                            check=lambda outs: [same(o, want) or sys.exit("graph mismatch c3 dequantize")
+                                                for o in outs])
+            res["dequantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_mxfp8"], ms,
+                                                                   traffic.get("dequantize_mxfp8"))}
+            log(f"c3 dequantize_mxfp8: {ms * 1e3:.2f} us")
+            del qs_, want
         if "c4" in configs:
             qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
             try:
@@ -286,6 +301,15 @@ def run_gpu(configs, steps, warmup, log):
         res["quantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["quantize_nvfp4"], ms, traffic.get("quantize_nvfp4"))}
         log(f"c5 quantize_nvfp4: {ms * 1e3:.2f} us")
         del as_
+        want = ck.dequantize_nvfp4(qa, ga, sa)
+        nset = _sets_for(BYTES["dequantize_nvfp4"])
+        qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
+        ms = time_graph(lambda i: (lambda: ck.dequantize_nvfp4(qs_[i][0], ga, qs_[i][1])), nset, steps, warmup,
+                        check=lambda outs: [same(o, want) or sys.exit("graph mismatch c5 dequantize") for o in outs])
+        res["dequantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_nvfp4"], ms,
+                                                               traffic.get("dequantize_nvfp4"))}
+        log(f"c5 dequantize_nvfp4: {ms * 1e3:.2f} us")
+        del qs_, want
         qw, sw = ck.quantize_nvfp4(w, gw)
         try:
             ref = ck.scaled_mm_nvfp4(qa, qw, ga, gw, sa, sw)
@@ -375,7 +399,8 @@ def pmc_sequence(configs, dev):
         x3 = make_c3(dev)
         qa, sa = ck.quantize_mxfp8(x3)
         if "c3" in configs:
-            seq.append(("quantize_mxfp8", lambda: ck.quantize_mxfp8(x3)))
+            seq += [("quantize_mxfp8", lambda: ck.quantize_mxfp8(x3)),
+                    ("dequantize_mxfp8", lambda: ck.dequantize_mxfp8(qa, sa))]
         if "c4" in configs:
             qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
             seq.append(("scaled_mm_mxfp8", lambda: ck.scaled_mm_mxfp8(qa, qw, sa, sw)))
@@ -384,6 +409,7 @@ def pmc_sequence(configs, dev):
         na, nsa = ck.quantize_nvfp4(a, ga)
         nw, nsw = ck.quantize_nvfp4(w, gw)
         seq += [("quantize_nvfp4", lambda: ck.quantize_nvfp4(a, ga)),
+                ("dequantize_nvfp4", lambda: ck.dequantize_nvfp4(na, ga, nsa)),
                 ("scaled_mm_nvfp4", lambda: ck.scaled_mm_nvfp4(na, nw, ga, gw, nsa, nsw))]
     return seq
 
@@ -421,7 +447,8 @@ def _pmc_dispatches(d: Path, counter: str):
 # kernel-name substring of each op's own dispatches (an op may launch several per call)
 OP_KERNELS = {"quantize_per_tensor_fp8": "ckh::quantize_fp8", "dequantize_per_tensor_fp8": "ckh::dequantize_fp8",
               "apply_rope": "ckh::rope", "apply_rope1": "ckh::rope", "quantize_mxfp8": "ckh::quantize_mxfp8",
-              "scaled_mm_mxfp8": "ckh::mx::gemm", "quantize_nvfp4": "ckh::quantize_nvfp4",
+              "dequantize_mxfp8": "ckh::dequantize_mxfp8", "scaled_mm_mxfp8": "ckh::mx::gemm",
+              "quantize_nvfp4": "ckh::quantize_nvfp4", "dequantize_nvfp4": "ckh::dequantize_nvfp4",
               "scaled_mm_nvfp4": "ckh::nv::gemm"}
 
 
@@ -463,11 +490,11 @@ def pmc_sequence_names(configs):
     if "c2" in configs:
         names += ["apply_rope", "apply_rope1"]
     if "c3" in configs:
-        names.append("quantize_mxfp8")
+        names += ["quantize_mxfp8", "dequantize_mxfp8"]
     if "c4" in configs:
         names.append("scaled_mm_mxfp8")
     if "c5" in configs:
-        names += ["quantize_nvfp4", "scaled_mm_nvfp4"]
+        names += ["quantize_nvfp4", "dequantize_nvfp4", "scaled_mm_nvfp4"]
     return [(n, None) for n in names]
 
 

@@ -185,6 +185,57 @@ def test_dequantize_mxfp8(out_dtype, hip, seed):
     assert torch.equal(bits(got), bits(want))
 
 
+def _same_or_both_nan(got: torch.Tensor, want: torch.Tensor) -> bool:
+    """Bit-exact except that a NaN only has to be a NaN: dequantizing a NaN code or scale,
+    or 0 * inf, gives the GPU's NaN payload, not the x86 payload of the CPU oracle."""
+    got = got.cpu()
+    nan_g, nan_w = torch.isnan(got.float()), torch.isnan(want.float())
+    return torch.equal(nan_g, nan_w) and torch.equal(bits(got)[~nan_w], bits(want)[~nan_w])
+
+
+def _misaligned(q: torch.Tensor, offset: int) -> torch.Tensor:
+    """q on the GPU at a data pointer `offset` bytes past a 16-byte boundary."""
+    buf = torch.zeros(q.numel() + offset, dtype=torch.uint8, device="cuda")
+    buf[offset:] = q.reshape(-1).view(torch.uint8).cuda()
+    return buf[offset:].view(q.dtype).view(q.shape)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_mxfp8_every_code_and_scale(out_dtype, hip, seed):
+    # raw bytes: every E4M3 code (NaN included) and every E8M0 scale (0 -> 0.0, 255 ->
+    # inf), 200 rows (padded scale rows); 16-bit outputs take the fast kernel, f32 output
+    # the general one, and an 8-byte-offset view of the codes runs either
+    rows, cols = 200, 320
+    q = torch.randint(0, 256, (rows, cols), dtype=torch.uint8)
+    q[0, :256] = torch.arange(256, dtype=torch.uint8)
+    e = torch.randint(0, 256, (rows, cols // 32), dtype=torch.uint8)
+    e.view(-1)[:256] = torch.arange(256, dtype=torch.uint8)
+    q = q.view(torch.float8_e4m3fn)
+    s = ref.to_blocked(e).view(torch.float8_e8m0fnu)
+    want = ref.dequantize_mxfp8(q, s, out_dtype)
+    assert _same_or_both_nan(ck.dequantize_mxfp8(q.cuda(), s.cuda(), out_dtype), want)
+    assert _same_or_both_nan(ck.dequantize_mxfp8(_misaligned(q, 8), s.cuda(), out_dtype), want)
+
+
+@pytest.mark.parametrize("hi_first", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cols", [320, 48])
+def test_dequantize_nvfp4_every_code_and_scale(cols, out_dtype, hi_first, hip, seed):
+    # raw bytes: every code byte and every E4M3 scale byte (NaN included); 16-bit outputs
+    # take the fast kernel, f32 output the general one; cols 48 leaves a partial wave
+    rows = 200
+    q = torch.randint(0, 256, (rows, cols // 2), dtype=torch.uint8)
+    q.view(-1)[:256] = torch.arange(256, dtype=torch.uint8)
+    e = torch.randint(0, 256, (rows, cols // 16), dtype=torch.uint8)
+    e.view(-1)[:256] = torch.arange(256, dtype=torch.uint8)
+    s = ref.to_blocked(e).view(torch.float8_e4m3fn)
+    for gv in [0.0123, 0.0, 3e38]:
+        g = torch.tensor([gv])
+        want = ref.dequantize_nvfp4(q, g, s, out_dtype, hi_first=hi_first)
+        got = ck.dequantize_nvfp4(q.cuda(), g.cuda(), s.cuda(), out_dtype, hi_first=hi_first)
+        assert _same_or_both_nan(got, want), gv
+
+
 # ----------------------------------------------------------------- NVFP4
 def _check_nv(x, g, pad, hi_first=True):
     want_q, want_s = ref.quantize_nvfp4(x, g, pad_16x=pad, hi_first=hi_first)
