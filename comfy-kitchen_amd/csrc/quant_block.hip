@@ -733,6 +733,51 @@ __global__ __launch_bounds__(kThreads) void dequantize_nvfp4_fast_kernel(const u
     }
 }
 
+// NVFP4 dequantize for cols % 256 == 0: a 512-thread workgroup takes the 32 rows whose
+// swizzled scale words share 128-byte lines (rows 8q..8q+7 of each 32-row group of a
+// 128-row tile) x 256 columns, so each scale line is read by one workgroup.  Wave
+// (w, h) takes rows 32w + 8q + 4h .. +3; lane l's piece p is piece 32 (2p + l/32) + l%32
+// of those 4 rows x 32 pieces, so each code load covers whole 128-byte row runs and each
+// store whole 512-byte row runs.
+template <int OUT, bool HI_FIRST>
+__global__ __launch_bounds__(512) void dequantize_nvfp4_tile_kernel(const uint8_t* __restrict__ qx,
+                                                                    const float* __restrict__ gptr,
+                                                                    const uint8_t* __restrict__ sc,
+                                                                    uint16_t* __restrict__ out, uint32_t rows,
+                                                                    uint32_t cols, uint32_t n_ct, uint32_t n_cb) {
+    const uint32_t b = blockIdx.x;
+    const uint32_t ct = b % n_ct, slice = b / n_ct;  // column tile; (128-row tile, q)
+    const uint32_t tile = slice >> 2, q = slice & 3;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t w = wave >> 1, h = wave & 1;
+    const float gr = round_to_hw<OUT>(gptr[0]);
+    uint32_t c[2], s8[2], r[2], cp[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        r[p] = tile * 128 + 32 * w + 8 * q + 4 * h + 2 * p + (lane >> 5);
+        cp[p] = ct * 32 + (lane & 31);  // 8-element piece of the row
+        c[p] = 0u;
+        s8[p] = 0u;
+        if (r[p] < rows) {
+            c[p] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(qx + static_cast<size_t>(r[p]) * (cols / 2)) + cp[p]);
+            const uint32_t blk = cp[p] >> 1;
+            s8[p] = sc[(((r[p] >> 7) * n_cb + (blk >> 2)) * 32 + (r[p] & 31)) * 16 + ((r[p] & 127) >> 5) * 4 + (blk & 3)];
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        if (r[p] >= rows) continue;
+        const float T = round_to_hw<OUT>(gr * hw_e4m3_to_f<0>(s8[p]));
+        float v[8];
+        nvfp4_pair<HI_FIRST, 0>(c[p], T, &v[0]);
+        nvfp4_pair<HI_FIRST, 1>(c[p], T, &v[2]);
+        nvfp4_pair<HI_FIRST, 2>(c[p], T, &v[4]);
+        nvfp4_pair<HI_FIRST, 3>(c[p], T, &v[6]);
+        store8_fast<OUT>(out + static_cast<size_t>(r[p]) * cols + static_cast<size_t>(cp[p]) * 8, v,
+                         !(__builtin_fabsf(T) < __builtin_inff()));
+    }
+}
+
 }  // namespace ckh
 
 using namespace ckh;
@@ -913,6 +958,24 @@ extern "C" int ckh_dequantize_nvfp4(const void* qx, const void* global_scale, co
     const float* g = static_cast<const float*>(global_scale);
     const uint8_t* s = static_cast<const uint8_t*>(scales);
     const bool hf = hi_first != 0;
+    if (out_code != CKH_F32 && cols % 256 == 0 && rows * cols < (int64_t(1) << 31)) {
+        const uint32_t n_ct = static_cast<uint32_t>(cols / 256);
+        const dim3 tgrid(static_cast<unsigned>(cdiv(rows, 128) * 4 * n_ct));
+        const uint32_t r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
+                       ncb = static_cast<uint32_t>(n_cb);
+        uint16_t* o = static_cast<uint16_t*>(out);
+#define LAUNCH_TILE(O, H) \
+    hipLaunchKernelGGL((dequantize_nvfp4_tile_kernel<O, H>), tgrid, dim3(512), 0, st, q, g, s, o, r32, c32, n_ct, ncb)
+        if (out_code == CKH_F16) {
+            if (hf) LAUNCH_TILE(CKH_F16, true);
+            else LAUNCH_TILE(CKH_F16, false);
+        } else {
+            if (hf) LAUNCH_TILE(CKH_BF16, true);
+            else LAUNCH_TILE(CKH_BF16, false);
+        }
+#undef LAUNCH_TILE
+        return check_launch("dequantize_nvfp4");
+    }
     const int64_t n_pieces = rows * (cols / 8);
     if (out_code != CKH_F32 && cols % 8 == 0 && n_pieces < (int64_t(1) << 31)) {
         uint32_t magic, shift;

@@ -219,10 +219,11 @@ def test_dequantize_mxfp8_every_code_and_scale(out_dtype, hip, seed):
 
 @pytest.mark.parametrize("hi_first", [True, False])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("cols", [320, 48])
+@pytest.mark.parametrize("cols", [320, 48, 512])
 def test_dequantize_nvfp4_every_code_and_scale(cols, out_dtype, hi_first, hip, seed):
     # raw bytes: every code byte and every E4M3 scale byte (NaN included); 16-bit outputs
-    # take the fast kernel, f32 output the general one; cols 48 leaves a partial wave
+    # take the 256-column tile kernel (cols 512; 200 rows end inside a 128-row tile) or
+    # the piece kernel (320, 48: a partial wave), f32 output the general one
     rows = 200
     q = torch.randint(0, 256, (rows, cols // 2), dtype=torch.uint8)
     q.view(-1)[:256] = torch.arange(256, dtype=torch.uint8)
