@@ -411,6 +411,8 @@ def pmc_sequence(configs, dev):
         seq += [("quantize_nvfp4", lambda: ck.quantize_nvfp4(a, ga)),
                 ("dequantize_nvfp4", lambda: ck.dequantize_nvfp4(na, ga, nsa)),
                 ("scaled_mm_nvfp4", lambda: ck.scaled_mm_nvfp4(na, nw, ga, gw, nsa, nsw))]
+    # --summarize-pmc walks the counter rows in the order pmc_sequence_names gives
+    assert [n for n, _ in seq] == [n for n, _ in pmc_sequence_names(configs)], "PMC sequence and names disagree"
     return seq
 
 
