@@ -413,9 +413,18 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 // the IEEE divisions.  The E2M1 convert saturates out-of-range inputs to +-6 exactly as
 // the reference's clamp (checked on all 2^32 non-NaN floats), so no clamp is needed.
 // Codes of a 16-element block by the exact division steps above (the guards hold).
-template <bool HI_FIRST>
+// RCP: y from v_rcp_f32 and one FMA Newton step, which equals the IEEE 1.0f / T for
+// every T significand at exponents -67, 0, 1 and 63 (checked exhaustively on gfx950),
+// i.e. across the common-block range T in [2^-69, 2^69]; otherwise an IEEE division.
+template <bool HI_FIRST, bool RCP = false>
 __device__ __forceinline__ uint2 nvfp4_codes16_exact(const float (&v)[16], float T) {
-    const float y = 1.0f / T;
+    float y;
+    if constexpr (RCP) {
+        const float y0 = __builtin_amdgcn_rcpf(T);
+        y = __builtin_fmaf(__builtin_fmaf(-T, y0, 1.0f), y0, y0);
+    } else {
+        y = 1.0f / T;
+    }
     float q[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
@@ -486,7 +495,7 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         // A row past the end has amax 0 and takes the general path.
         if (g_ok && amax >= 0x1p-60f && amax <= 0x1p60f && cf <= 448.0f && s8f != 0u) {
             s8 = s8f;
-            codes = nvfp4_codes16_exact<HI_FIRST>(v, g * hw_e4m3_to_f<0>(s8f));
+            codes = nvfp4_codes16_exact<HI_FIRST, true>(v, g * hw_e4m3_to_f<0>(s8f));
         } else {
             const float c = g_ok && amax >= 0x1p-60f && amax <= 0x1p60f ? cf : nvfp4_c_div_rare(amax, g);
             s8 = r[u] < rows ? nvfp4_scale_code_of(c, amax, g) : 0u;
