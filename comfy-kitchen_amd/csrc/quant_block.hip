@@ -414,8 +414,8 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 // the reference's clamp (checked on all 2^32 non-NaN floats), so no clamp is needed.
 // Codes of a 16-element block by the exact division steps above (the guards hold).
 // RCP: y from v_rcp_f32 and one FMA Newton step, which equals the IEEE 1.0f / T for
-// every T significand at exponents -67, 0, 1 and 63 (checked exhaustively on gfx950),
-// i.e. across the common-block range T in [2^-69, 2^69]; otherwise an IEEE division.
+// every T in [2^-70, 2^71) (checked exhaustively on gfx950), covering the common-block
+// range T in [2^-69, 2^69]; otherwise an IEEE division.
 template <bool HI_FIRST, bool RCP = false>
 __device__ __forceinline__ uint2 nvfp4_codes16_exact(const float (&v)[16], float T) {
     float y;
