@@ -459,7 +459,10 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     const uint32_t l = threadIdx.x & 3;
     const float g = gptr[0];
     const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
-    const float yg = 1.0f / g;
+    // RN(1/g) by rcp + one Newton step: equal to the IEEE division for every g in
+    // [2^-70, 2^71), and yg is only used when g_ok
+    const float yg0 = __builtin_amdgcn_rcpf(g);
+    const float yg = __builtin_fmaf(__builtin_fmaf(-g, yg0, 1.0f), yg0, yg0);
     constexpr float y6 = 1.0f / 6.0f;
     uint4 w[kNvUnits][2];
     uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
