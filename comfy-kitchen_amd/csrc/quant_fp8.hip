@@ -36,12 +36,15 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
                                                                 const float* __restrict__ scale,
                                                                 uint8_t* __restrict__ out, int64_t n) {
     const float r = round_to<IN>(1.0f / scale[0]);
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kPerThread;
+    // a wave's 1024 elements: lane l takes the 8-element pieces l and 64 + l, so every load
+    // and store instruction covers one contiguous run
+    const int64_t wbase = (static_cast<int64_t>(blockIdx.x) * kThreads + (threadIdx.x & ~63u)) * kPerThread;
+    const int64_t ia = wbase + 8 * (threadIdx.x & 63u), ib = ia + 512;
     constexpr int ES = ElemSize<IN>::value;
-    if (VEC && i0 + kPerThread <= n) {
+    if (VEC && ib + 8 <= n) {
         float v[16];
-        load8<IN>(static_cast<const char*>(x) + i0 * ES, *reinterpret_cast<float(*)[8]>(&v[0]));
-        load8<IN>(static_cast<const char*>(x) + (i0 + 8) * ES, *reinterpret_cast<float(*)[8]>(&v[8]));
+        load8<IN>(static_cast<const char*>(x) + ia * ES, *reinterpret_cast<float(*)[8]>(&v[0]));
+        load8<IN>(static_cast<const char*>(x) + ib * ES, *reinterpret_cast<float(*)[8]>(&v[8]));
         // hardware path: product rounded to x's dtype, clamped, converted in pairs
         float t[16];
         bool any_nan = false;
@@ -68,9 +71,12 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
                 w[q] = acc;
             }
         }
-        st_stream16(out + i0, make_uint4(w[0], w[1], w[2], w[3]));
+        st_stream8(out + ia, make_uint2(w[0], w[1]));
+        st_stream8(out + ib, make_uint2(w[2], w[3]));
     } else {
-        for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i)
+        for (int64_t i = ia; i < n && i < ia + 8; ++i)
+            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+        for (int64_t i = ib; i < n && i < ib + 8; ++i)
             out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
     }
 }
@@ -87,47 +93,38 @@ __device__ __forceinline__ void store_out(void* out, int64_t i, float v) {
     else reinterpret_cast<uint16_t*>(out)[i] = static_cast<uint16_t>(f_to_f16(v));
 }
 
-// Store 16 rounded outputs starting at element i (16-byte aligned), 16-bit outputs
-// rounded by the hardware converts (callers route NaN-containing data elsewhere).
+// Store 16 rounded outputs: v[0..7] at element i, v[8..15] at element j (each 16-byte
+// aligned); 16-bit outputs rounded by the hardware converts (callers route NaN-containing
+// data elsewhere).
 template <int OUT>
-__device__ __forceinline__ void store16_hw(void* out, int64_t i, const float (&v)[16]) {
+__device__ __forceinline__ void store16_hw(void* out, int64_t i, int64_t j, const float (&v)[16]) {
     if constexpr (OUT == CKH_F32) {
         float* p = static_cast<float*>(out) + i;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            st_stream16(p + 4 * q, make_uint4(as_u(v[4 * q]), as_u(v[4 * q + 1]), as_u(v[4 * q + 2]), as_u(v[4 * q + 3])));
+        float* q = static_cast<float*>(out) + j;
+        st_stream16(p, make_uint4(as_u(v[0]), as_u(v[1]), as_u(v[2]), as_u(v[3])));
+        st_stream16(p + 4, make_uint4(as_u(v[4]), as_u(v[5]), as_u(v[6]), as_u(v[7])));
+        st_stream16(q, make_uint4(as_u(v[8]), as_u(v[9]), as_u(v[10]), as_u(v[11])));
+        st_stream16(q + 4, make_uint4(as_u(v[12]), as_u(v[13]), as_u(v[14]), as_u(v[15])));
     } else {
         uint32_t w[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * q]) : f_to_f16(v[2 * q]);
-            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
-            w[q] = lo | (hi << 16);
+        for (int k = 0; k < 8; ++k) {
+            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * k]) : f_to_f16(v[2 * k]);
+            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16_rne(v[2 * k + 1]) : f_to_f16(v[2 * k + 1]);
+            w[k] = lo | (hi << 16);
         }
-        uint16_t* p = static_cast<uint16_t*>(out) + i;
-        st_stream16(p, make_uint4(w[0], w[1], w[2], w[3]));
-        st_stream16(p + 8, make_uint4(w[4], w[5], w[6], w[7]));
+        st_stream16(static_cast<uint16_t*>(out) + i, make_uint4(w[0], w[1], w[2], w[3]));
+        st_stream16(static_cast<uint16_t*>(out) + j, make_uint4(w[4], w[5], w[6], w[7]));
     }
 }
 
-// Store 16 rounded outputs starting at element i (16-byte aligned).
+// The same with the software converts (keeps the software's NaN bits).
 template <int OUT>
-__device__ __forceinline__ void store16(void* out, int64_t i, const float (&v)[16]) {
-    if constexpr (OUT == CKH_F32) {
-        float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+__device__ __forceinline__ void store16(void* out, int64_t i, int64_t j, const float (&v)[16]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-    } else {
-        uint32_t w[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            uint32_t lo = OUT == CKH_BF16 ? f_to_bf16(v[2 * q]) : f_to_f16(v[2 * q]);
-            uint32_t hi = OUT == CKH_BF16 ? f_to_bf16(v[2 * q + 1]) : f_to_f16(v[2 * q + 1]);
-            w[q] = lo | (hi << 16);
-        }
-        uint4* p = reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + i);
-        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    for (int k = 0; k < 8; ++k) {
+        store_out<OUT>(out, i + k, v[k]);
+        store_out<OUT>(out, j + k, v[8 + k]);
     }
 }
 
@@ -136,10 +133,15 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
                                                                   const float* __restrict__ scale,
                                                                   void* __restrict__ out, int64_t n) {
     const float s = round_to<OUT>(scale[0]);
-    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kPerThread;
-    if (VEC && i0 + kPerThread <= n) {
-        uint4 c = ld_stream16(x + i0);
-        uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+    // a wave's 1024 codes: lane l takes the 8-code pieces l and 64 + l, so every load and
+    // store instruction covers one contiguous run
+    const int64_t wbase = (static_cast<int64_t>(blockIdx.x) * kThreads + (threadIdx.x & ~63u)) * kPerThread;
+    const int64_t ia = wbase + 8 * (threadIdx.x & 63u), ib = ia + 512;
+    if (VEC && ib + 8 <= n) {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 ca = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ia));
+        const u32x2 cb = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ib));
+        uint32_t cw[4] = {ca.x, ca.y, cb.x, cb.y};
         // a NaN code (0x7f / 0xff in E4M3) takes the software path, which fixes its bytes
         bool nan_code = false;
 #pragma unroll
@@ -157,14 +159,15 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
                 v[4 * q + 2] = hw_e4m3_to_f<2>(cw[q]) * s;
                 v[4 * q + 3] = hw_e4m3_to_f<3>(cw[q]) * s;
             }
-            store16_hw<OUT>(out, i0, v);
+            store16_hw<OUT>(out, ia, ib, v);
         } else {
 #pragma unroll
             for (int j = 0; j < 16; ++j) v[j] = decode_fp8<IN>((cw[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
-            store16<OUT>(out, i0, v);
+            store16<OUT>(out, ia, ib, v);
         }
     } else {
-        for (int64_t i = i0; i < n && i < i0 + kPerThread; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
+        for (int64_t i = ia; i < n && i < ia + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
+        for (int64_t i = ib; i < n && i < ib + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
     }
 }
 
