@@ -208,7 +208,7 @@ def load_traffic() -> dict:
 def run_gpu(configs, steps, warmup, log):
     import comfy_kitchen as ck
 
-    from oracle import eager_ref  # checker only: verifies graph replays against the oracle on a slice
+    # Each timed graph's replay is checked, bit for bit, against the same op called eagerly.
     dev = torch.device("cuda", 0)
     res = {}
     traffic = load_traffic()
@@ -245,7 +245,9 @@ def run_gpu(configs, steps, warmup, log):
                         check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
         res["apply_rope"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope"], ms, traffic.get("apply_rope"))}
         log(f"c2 apply_rope: {ms * 1e3:.2f} us")
-        ms = time_graph(lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup)
+        rq1 = ck.apply_rope1(q, f)
+        ms = time_graph(lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
+                        check=lambda outs: [same(o, rq1) or sys.exit("graph mismatch c2 rope1") for o in outs])
         res["apply_rope1"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope1"], ms, traffic.get("apply_rope1"))}
         log(f"c2 apply_rope1: {ms * 1e3:.2f} us")
         del qs, ks

@@ -1,8 +1,12 @@
 // Dynamic per-tensor scale on the device: scale = amax(|x|) / divisor, computed in x's
 // dtype and widened to fp32.  This is the default scale of the layouts' quantize
 // (reference tensor/fp8.py:56-61: torch.amax(tensor.abs()) / finfo(e4m3).max, and
-// tensor/nvfp4.py:64-69: ... / (448 * 6)): a 0-dim tensor of x's dtype, i.e. the fp32
-// quotient of the (exact) amax and the divisor rounded once to x's dtype.
+// tensor/nvfp4.py:64-69: ... / (448 * 6)): a 0-dim tensor of x's dtype.  torch evaluates
+// that division on a GPU tensor by a Python-scalar divisor as a multiply by the fp32
+// reciprocal: RN32(amax * RN32(1/divisor)), rounded once to x's dtype.  The kernel does the
+// same (the reciprocal is formed on the host in fp32), so it matches the reference on the
+// device bit for bit; a true division differs from it in the last fp32 bit for about half
+// of all fp32 amaxes and for some tiny f16 ones.
 //
 // Two launches on the caller's stream, no allocation and no host synchronisation, so
 // the scale feeds the quantize kernels (which read it from device memory) directly:
@@ -97,15 +101,15 @@ __global__ __launch_bounds__(kThreads) void amax_kernel(const void* __restrict__
     if (threadIdx.x == 0) partial[blockIdx.x] = b;
 }
 
-// *out = float(round_IN(amax / divisor)), amax = the largest of the nblocks partial words
+// *out = float(round_IN(amax * inv_divisor)), amax = the largest of the nblocks partial words
 template <int IN>
 __global__ __launch_bounds__(kThreads) void finalize_kernel(const uint32_t* __restrict__ partial, int nblocks,
-                                                            float divisor, float* __restrict__ out) {
+                                                            float inv_divisor, float* __restrict__ out) {
     uint32_t m = 0;
     for (int i = threadIdx.x; i < nblocks; i += kThreads) m = max(m, partial[i]);
     const uint32_t b = block_max(m);
     if (threadIdx.x == 0) {
-        const float q = as_f(b) / divisor;
+        const float q = as_f(b) * inv_divisor;
         float r;
         if constexpr (IN == CKH_BF16) r = bf16_to_f(f_to_bf16(q));
         else if constexpr (IN == CKH_F16) r = round_f16(q);
@@ -128,6 +132,8 @@ extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float d
     CKH_REQUIRE(aligned(scale_out, 4) && aligned(workspace, 4), "amax_scale: output or workspace misaligned");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint32_t* partial = static_cast<uint32_t*>(workspace);
+    // torch's op-math reciprocal of the scalar divisor: fp32 division on the host
+    const float inv_divisor = 1.0f / divisor;
     const int es = in_code == CKH_F32 ? 4 : 2;
     const bool vec = aligned(x, 16);
     // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight
@@ -138,7 +144,7 @@ extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float d
     do {                                                                                                     \
         if (vec) hipLaunchKernelGGL((am::amax_kernel<I, true>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
         else hipLaunchKernelGGL((am::amax_kernel<I, false>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
-        hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(am::kThreads), 0, st, partial, blocks, divisor, \
+        hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(am::kThreads), 0, st, partial, blocks, inv_divisor, \
                            static_cast<float*>(scale_out));                                                  \
     } while (0)
     if (in_code == CKH_F32) LAUNCH(CKH_F32);

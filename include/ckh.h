@@ -95,7 +95,8 @@ int ckh_dequantize_mxfp8(const void* qx, const void* scales, void* out, int64_t 
 /*
  * NVFP4 quantize of x [orig_rows, orig_cols] with device f32 global scale g into packed
  * E2M1 codes [rows, cols/2] u8 and E4M3 block-16 scales, swizzled
- * [roundup(rows,128), roundup(cols/16,4)].  rows % 16 == 0, cols % 16 == 0.
+ * [roundup(rows,128), roundup(cols/16,4)].  cols % 16 == 0 (rows need not be a
+ * multiple of anything; the layouts pad them to 16 as the reference's pad_16x does).
  * epsilon is accepted and ignored, as in the reference.
  * Replaces launch_quantize_nvfp4_kernel (dlpack_bindings.cpp:104-116,
  * ops/quantize_nvfp4.cu:323-384); arithmetic follows eager quantization.py:115-160.
@@ -158,7 +159,7 @@ int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const 
  * NVFP4 GEMM: out[M,N] = alpha * sum_k E2M1(a)*sa[m,k/16] * E2M1(b)*sb[n,k/16] (+bias[n]).
  * a [M,K/2] u8, b [N,K/2] u8 (hi_first packing), sa/sb E4M3 swizzled with logical
  * shapes [M, K/16] / [N, K/16]; alpha one f32 on device; bias NULL or [N].
- * K % 64 == 0.
+ * K % 32 == 0.
  * Replaces launch_cublas_gemm_blockwise_fp4_kernel (dlpack_bindings.cpp:59-74,
  * ops/cublas_gemm_nvfp4.cu:297-342); semantics follow eager quantization.py:222-246.
  */
@@ -168,9 +169,10 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
                         uintptr_t stream);
 
 /*
- * Dynamic per-tensor scale: *scale_out = float(round_x(amax(|x|) / divisor)), the amax
- * and the quotient rounded to x's dtype (in_code), as the layouts' default scale
- * torch.amax(tensor.abs()) / max computes it.  x: numel contiguous elements; scale_out:
+ * Dynamic per-tensor scale: *scale_out = float(round_x(amax(|x|) * RN32(1/divisor))),
+ * the amax and the product rounded to x's dtype (in_code), as the layouts' default scale
+ * torch.amax(tensor.abs()) / max computes it on a GPU tensor (torch multiplies by the
+ * fp32 reciprocal of a scalar divisor there).  x: numel contiguous elements; scale_out:
  * one f32 on device; workspace: CKH_AMAX_WORKSPACE_BYTES of device memory (4-byte
  * aligned, contents ignored and overwritten) that holds the per-workgroup partial maxima,
  * so the call allocates nothing.  Calls running at the same time need workspaces of their

@@ -41,6 +41,8 @@ def load():
     lib.ref_quantize_fp8_bf16.restype, lib.ref_quantize_fp8_bf16.argtypes = None, [p, i64, f32, i32, p]
     lib.ref_quantize_mxfp8_row_bf16.restype, lib.ref_quantize_mxfp8_row_bf16.argtypes = None, [p, i64, p, p]
     lib.ref_quantize_nvfp4_row_bf16.restype, lib.ref_quantize_nvfp4_row_bf16.argtypes = None, [p, i64, f32, p, p]
+    lib.ref_default_scale.restype, lib.ref_default_scale.argtypes = f32, [f32, f32, i32]
+    lib.ref_dequantize_nvfp4_value.restype, lib.ref_dequantize_nvfp4_value.argtypes = f32, [i32, i32, f32, i32]
     return lib
 
 

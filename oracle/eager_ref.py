@@ -18,6 +18,8 @@ torch CPU routines in the same order, so its results are the eager backend's:
   to_blocked / from_blocked  float_utils.py:292-352
   e8m0_to_f32                float_utils.py:376-382
   apply_rope1 / apply_rope   backends/eager/rope.py:7-18
+  default_scale              tensor/fp8.py:56-61, tensor/nvfp4.py:64-69 (as evaluated
+                             on a GPU tensor: multiply by the fp32 reciprocal)
   scaled_mm_*_ref            closed form: fp32 matmul of the dequantized operands
                              (eager routes to torch F.scaled_mm, which has no CPU
                              kernel; quantization.py:222-246, 367-402)
@@ -26,6 +28,9 @@ How it is pinned (tests/test_oracle.py): against oracle/scalar_ref.c, an indepen
 scalar C implementation that rounds by brute-force nearest-value search rather than
 bit tricks, exhaustively over every bf16 input pattern; against the golden vectors in
 tests/golden/; and against closed-form invariants (swizzle round trips, nibble swap).
+default_scale is also checked on the GPU against torch's own device kernel
+(tests/test_gpu_quant.py), and dequantize_nvfp4's rounding of the block total in the
+output dtype against hand-derived known answers and ref_dequantize_nvfp4_value.
 """
 from __future__ import annotations
 
@@ -72,8 +77,17 @@ def e8m0_to_f32(x: torch.Tensor) -> torch.Tensor:
 # ------------------------------------------------------------- per-tensor FP8
 def default_scale(x: torch.Tensor, max_value: float) -> torch.Tensor:
     """The layouts' default per-tensor scale (tensor/fp8.py:56-61, tensor/nvfp4.py:64-69):
-    torch.amax(x.abs()) / max_value in x's dtype, then cast to fp32 (a 0-dim tensor)."""
-    return (torch.amax(x.abs()) / max_value).to(torch.float32)
+    torch.amax(x.abs()) / max_value, a 0-dim tensor of x's dtype, then cast to fp32.
+
+    Restated as torch evaluates it on the GPU tensor the layout holds: a true divide by a
+    Python-scalar divisor runs as a multiply by the divisor's fp32 reciprocal in fp32 (the
+    op-math type of f32/f16/bf16), rounded once to x's dtype.  torch's CPU kernel divides
+    instead; the two agree on every bf16 amax but not on about half of fp32 amaxes or on
+    39 tiny f16 amaxes (tests/golden/known_answers.json "default_scale" has examples).
+    """
+    amax = torch.amax(x.abs()).to(torch.float32)
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(max_value, dtype=torch.float32)
+    return (amax * inv).to(x.dtype).to(torch.float32)
 
 
 def quantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,

@@ -149,3 +149,83 @@ void ref_quantize_nvfp4_row_bf16(const uint16_t* x, int64_t nblk, float g, uint8
         }
     }
 }
+
+/* ---- 16-bit float formats by value (out code 1 = f16, 2 = bf16) */
+static double ref_value16(int code, unsigned h) {
+    double v;
+    if (code == 2) {
+        v = (double)f_from_bits((uint32_t)(h & 0x7fff) << 16);
+    } else {
+        int e = (h >> 10) & 31, m = h & 1023;
+        if (e == 31) v = m ? NAN : INFINITY;
+        else v = e ? ldexp(1.0 + m / 1024.0, e - 15) : ldexp(m / 1024.0, -14);
+    }
+    return (h & 0x8000) ? -v : v;
+}
+
+/* nearest 16-bit code to v, ties to the even code: binary search over the positive
+ * finite codes, whose values increase with the code, then the nearer of the two that
+ * bracket |v|.  Past the largest finite value the next binade's first value stands for
+ * infinity: |v| at or above the midpoint between the two rounds to inf (the largest
+ * finite code is odd, so the tie goes to inf as well). */
+static unsigned ref_round16(int code, double v) {
+    unsigned lo = 0, hi = code == 2 ? 0x7f7f : 0x7bff;
+    double a = fabs(v);
+    double top = ref_value16(code, hi), past = code == 2 ? ldexp(1.0, 128) : ldexp(1.0, 16);
+    if (a >= (top + past) / 2) return (signbit(v) ? 0x8000u : 0u) | (hi + 1);
+    while (hi - lo > 1) {
+        unsigned mid = (lo + hi) / 2;
+        if (ref_value16(code, mid) <= a) lo = mid; else hi = mid;
+    }
+    double dl = a - ref_value16(code, lo), dh = ref_value16(code, hi) - a;
+    unsigned c = (dl < dh || (dl == dh && (lo & 1) == 0)) ? lo : hi;
+    return (signbit(v) ? 0x8000u : 0u) | c;
+}
+
+/* nearest fp32 to a double that is exact in double precision (products of two floats),
+ * ties to even, by comparing the float neighbours of a first guess */
+static float ref_nearest_f32(double p) {
+    float c = (float)p, best = c;
+    double bd = fabs(p - (double)c);
+    float cand[2] = {nextafterf(c, -INFINITY), nextafterf(c, INFINITY)};
+    for (int i = 0; i < 2; ++i) {
+        double d = fabs(p - (double)cand[i]);
+        if (d < bd || (d == bd && (bits_of(cand[i]) & 1u) == 0)) { bd = d; best = cand[i]; }
+    }
+    return best;
+}
+
+/* RN32(1/d): the float c nearest 1/d, i.e. with the smallest |c*d - 1| (c*d is exact) */
+static float ref_recip_f32(float d) {
+    float c = (float)(1.0 / (double)d), best = c;
+    double bd = fabs((double)c * d - 1.0);
+    float cand[2] = {nextafterf(c, -INFINITY), nextafterf(c, INFINITY)};
+    for (int i = 0; i < 2; ++i) {
+        double e = fabs((double)cand[i] * d - 1.0);
+        if (e < bd || (e == bd && (bits_of(cand[i]) & 1u) == 0)) { bd = e; best = cand[i]; }
+    }
+    return best;
+}
+
+/* ---- the layouts' default scale, torch.amax(x.abs()) / divisor on a GPU tensor
+ * (tensor/fp8.py:56-61, tensor/nvfp4.py:64-69): amax * RN32(1/divisor) rounded to fp32,
+ * then to x's dtype (in_code 0 = f32, 1 = f16, 2 = bf16); returned widened to fp32. */
+float ref_default_scale(float amax, float divisor, int in_code) {
+    float p = ref_nearest_f32((double)amax * (double)ref_recip_f32(divisor));
+    if (in_code == 0) return p;
+    return (float)ref_value16(in_code, ref_round16(in_code, (double)p));
+}
+
+/* ---- one dequantized NVFP4 element (quantization.py:208-214): the block total
+ * g.to(out) * s8.to(out) and the product with the E2M1 value are each rounded to the
+ * output dtype (out_code 0 = f32, 1 = f16, 2 = bf16). */
+float ref_dequantize_nvfp4_value(int code4, int s8, float g, int out_code) {
+    double e = ref_e2m1_value(code4), s = ref_e4m3_value(s8);
+    if (out_code == 0) {
+        float t = ref_nearest_f32((double)g * s);
+        return ref_nearest_f32(e * (double)t);
+    }
+    double gt = ref_value16(out_code, ref_round16(out_code, (double)g));
+    double t = ref_value16(out_code, ref_round16(out_code, gt * s));
+    return (float)ref_value16(out_code, ref_round16(out_code, e * t));
+}

@@ -80,3 +80,34 @@ def unpack(packed: torch.Tensor, hi_first: bool = True) -> list[int]:
         hi, lo = b >> 4, b & 15
         out += [hi, lo] if hi_first else [lo, hi]
     return out
+
+
+_CODES = {"f32": 0, "f16": 1, "bf16": 2}
+_DTYPES = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def default_scale_cases():
+    """(amax tensor [1] of the input dtype, dtype code, divisor, expected fp32 scale bits)"""
+    res = []
+    for c in _load()["default_scale"]:
+        x = torch.tensor([c["amax"]], dtype=torch.float64).to(_DTYPES[c["dtype"]])
+        assert float(x) == c["amax"], "known-answer amax must be exact in its dtype"
+        res.append((x, _CODES[c["dtype"]], float(c["divisor"]), int(c["scale_bits"], 16)))
+    return res
+
+
+def dequantize_nvfp4_cases():
+    """(output dtype, dtype code, g f32 [1], scale byte, E2M1 code, expected 16-bit output bits)"""
+    res = []
+    for c in _load()["dequantize_nvfp4"]:
+        res.append((_DTYPES[c["out"]], _CODES[c["out"]], torch.tensor([c["g"]], dtype=torch.float32),
+                    int(c["scale"], 16), int(c["code"]), int(c["value_bits"], 16)))
+    return res
+
+
+def nvfp4_block(code: int, scale_byte: int, hi_first: bool = True):
+    """One NVFP4 block of 16 equal codes: packed [1, 8] uint8 and swizzled E4M3 [128, 4]."""
+    q = torch.full((1, 8), (code << 4) | code, dtype=torch.uint8)
+    s = torch.zeros(128, 4, dtype=torch.uint8)
+    s[0, 0] = scale_byte  # logical (0, 0) is swizzled byte 0
+    return q, s.view(torch.float8_e4m3fn)

@@ -327,6 +327,16 @@ def test_dequantize_nvfp4(out_dtype, hi_first, hip, seed):
     assert torch.equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("case", range(len(kat.dequantize_nvfp4_cases())))
+@pytest.mark.parametrize("hi_first", [True, False])
+def test_dequantize_nvfp4_known_answers(case, hi_first, hip):
+    """The block total and the element product round in the output dtype."""
+    dt, _, g, sbyte, c4, want = kat.dequantize_nvfp4_cases()[case]
+    q, s = kat.nvfp4_block(c4, sbyte)
+    out = ck.dequantize_nvfp4(q.cuda(), g.cuda(), s.cuda(), dt, hi_first=hi_first)
+    assert set((bits(out).int() & 0xFFFF).reshape(-1).tolist()) == {want}
+
+
 # ------------------------------------------------------------ dynamic scales
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("n", [1, 7, 4096, 1000003, 4096 * 3072])
@@ -337,6 +347,33 @@ def test_amax_scale_matches_torch(dtype, n, divisor, hip, seed):
     got = ck.amax_scale(x.cuda(), divisor)
     assert got.shape == () and got.dtype == torch.float32
     assert torch.equal(got.cpu().view(torch.int32), want.view(torch.int32))
+    # the reference expression itself, evaluated by torch on the device (tensor/fp8.py:57)
+    on_device = (torch.amax(x.cuda().abs()) / divisor).float()
+    assert torch.equal(got.cpu().view(torch.int32), on_device.cpu().view(torch.int32))
+
+
+@pytest.mark.parametrize("case", range(len(kat.default_scale_cases())))
+def test_amax_scale_known_answers(case, hip):
+    x, _, divisor, want = kat.default_scale_cases()[case]
+    xs = torch.cat([x, -x / 2, x * 0]).cuda()
+    got = ck.amax_scale(xs, divisor)
+    assert int(got.view(torch.int32).cpu()) & 0xFFFFFFFF == want
+
+
+@pytest.mark.parametrize("divisor", [448.0, 57344.0])
+def test_amax_scale_tiny_f16_follows_the_device_division(divisor, hip):
+    """The f16 amaxes whose quotient torch's CPU and GPU kernels round differently: the
+    kernel gives the GPU's (reciprocal-multiply) value, as the oracle does."""
+    f16 = torch.arange(0, 0x7C00, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    cpu_div = (f16 / divisor).float()
+    dev_div = (f16.cuda() / divisor).float().cpu()
+    split = f16[cpu_div.view(torch.int32) != dev_div.view(torch.int32)]
+    assert 0 < split.numel() < 100
+    for v in split:
+        x = torch.stack([v, -v]).cuda()
+        got = ck.amax_scale(x, divisor).cpu()
+        assert torch.equal(got.view(torch.int32), (torch.amax(x.abs()) / divisor).float().cpu().view(torch.int32))
+        assert torch.equal(got.view(torch.int32), ref.default_scale(x.cpu(), divisor).view(torch.int32))
 
 
 @pytest.mark.parametrize("n", [8192 * 5120, 8192 * 5120 + 5])

@@ -72,6 +72,70 @@ def test_kat_nvfp4_oracle_and_scalar(case, scalar_ref):
     assert int(sc[0]) == want_scale and c.tolist() == want_codes
 
 
+@pytest.mark.parametrize("case", range(len(kat.default_scale_cases())))
+def test_kat_default_scale_oracle_and_scalar(case, scalar_ref):
+    """The layouts' default scale: rounded to x's dtype, and formed as amax * RN32(1/d)
+    as torch's GPU kernel does.  A scale kept in fp32, or a true division, fails."""
+    x, code, divisor, want = kat.default_scale_cases()[case]
+    got = ref.default_scale(x, divisor)
+    assert got.dtype == torch.float32 and got.shape == ()
+    assert int(got.view(torch.int32)) & 0xFFFFFFFF == want
+    s = scalar_ref.ref_default_scale(float(x), divisor, code)
+    assert int(np.float32(s).view(np.uint32)) == want
+
+
+@pytest.mark.parametrize("case", range(len(kat.dequantize_nvfp4_cases())))
+@pytest.mark.parametrize("hi_first", [True, False])
+def test_kat_dequantize_nvfp4_oracle_and_scalar(case, hi_first, scalar_ref):
+    """The block total g.to(out) * s8.to(out) and the element product round in the output
+    dtype; forming either in fp32 gives a different last bit for these cases."""
+    dt, code, g, sbyte, c4, want = kat.dequantize_nvfp4_cases()[case]
+    q, s = kat.nvfp4_block(c4, sbyte)
+    out = ref.dequantize_nvfp4(q, g, s, dt, hi_first=hi_first)
+    assert out.shape == (1, 16)
+    assert set((out.view(torch.int16).int() & 0xFFFF).tolist()[0]) == {want}
+    v = scalar_ref.ref_dequantize_nvfp4_value(c4, sbyte, float(g), code)
+    assert int(torch.tensor(v).to(dt).view(torch.int16)) & 0xFFFF == want
+
+
+def _all16(dt):
+    return torch.arange(65536, dtype=torch.int32).to(torch.int16).view(dt)
+
+
+@pytest.mark.parametrize("divisor", [448.0, 2688.0, 57344.0])
+def test_default_scale_oracle_vs_scalar(divisor, scalar_ref):
+    """Every tiny f16 amax (where torch's device and CPU kernels disagree), a bf16 and
+    an f32 sample, each as a one-element tensor through the oracle's expression."""
+    g = torch.Generator().manual_seed(3)
+    f16 = _all16(torch.float16)
+    f16 = f16[(f16.float().abs() < 0.06) & (f16.float() >= 0)]
+    bf16 = _all16(torch.bfloat16)
+    bf16 = bf16[torch.isfinite(bf16.float()) & (bf16.float() >= 0)]
+    bf16 = bf16[torch.randperm(bf16.numel(), generator=g)[:3000]]
+    f32 = (torch.rand(3000, generator=g) * 2 ** torch.randint(-40, 40, (3000,), generator=g).float())
+    for t, code in ((f16, 1), (bf16, 2), (f32, 0)):
+        for v in t:
+            got = ref.default_scale(v.reshape(1), divisor)
+            want = scalar_ref.ref_default_scale(abs(float(v)), divisor, code)
+            assert int(got.view(torch.int32)) == int(np.float32(want).view(np.int32)), (code, float(v))
+
+
+@pytest.mark.parametrize("out_dtype, code", [(torch.bfloat16, 2), (torch.float16, 1), (torch.float32, 0)])
+def test_dequantize_nvfp4_oracle_vs_scalar(out_dtype, code, scalar_ref):
+    """Every E2M1 code x every finite E4M3 scale byte, for a few global scales."""
+    codes = torch.arange(16, dtype=torch.uint8)
+    for g in (1.005859375, 1.000732421875, 0.0123, 3e-3, 77.7):
+        for sbyte in range(0, 0x7F):
+            vals = [scalar_ref.ref_dequantize_nvfp4_value(c, sbyte, g, code) for c in range(16)]
+            q = ((codes[0::2] << 4) | codes[1::2]).reshape(1, 8)
+            s = torch.zeros(128, 4, dtype=torch.uint8)
+            s[0, 0] = sbyte
+            out = ref.dequantize_nvfp4(q, torch.tensor([g]), s.view(torch.float8_e4m3fn), out_dtype)
+            want = torch.tensor(vals).to(out_dtype)
+            assert torch.equal(out.reshape(16).view(torch.int16 if code else torch.int32),
+                               want.view(torch.int16 if code else torch.int32)), (g, sbyte)
+
+
 # -------------------------------------------------- exhaustive vs scalar C
 @pytest.mark.parametrize("out_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
 @pytest.mark.parametrize("scale", [1.0, 0.9481481481481482, 10.0 / 448, 2.0 ** -20, 3.0e4, 0.7])
