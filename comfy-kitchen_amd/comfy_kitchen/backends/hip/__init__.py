@@ -58,8 +58,9 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_scaled_mm_fp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _p, _u64]),
+    "ckh_amax_scale_noalloc": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 # CKH_AMAX_WORKSPACE_BYTES of include/ckh.h: the workspace ckh_amax_scale takes
 AMAX_WORKSPACE_BYTES = 8192
 

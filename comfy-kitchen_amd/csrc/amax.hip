@@ -19,6 +19,9 @@
 // pass 1 of the same call.  Pass 1 reads x with ordinary (cached) loads, kUnroll 16-byte
 // loads in flight per thread: the quantize kernel that follows finds the tensor in the
 // 256 MB infinity cache when it fits there.
+#include <atomic>
+#include <mutex>
+
 #include "ckh_common.h"
 
 namespace ckh {
@@ -123,20 +126,17 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const uint32_t* __re
 
 using namespace ckh;
 
-extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
-                              void* workspace, uintptr_t stream) {
-    CKH_REQUIRE(x && scale_out && workspace, "amax_scale: null pointer");
-    CKH_REQUIRE(numel > 0, "amax_scale: empty tensor (torch.amax of an empty tensor is an error too)");
-    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
-                "amax_scale: unsupported input dtype code %d", in_code);
-    CKH_REQUIRE(aligned(scale_out, 4) && aligned(workspace, 4), "amax_scale: output or workspace misaligned");
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    uint32_t* partial = static_cast<uint32_t*>(workspace);
+namespace {
+
+// Both entry points: pass 1 (per-workgroup maxima into `partial`) and pass 2 (the scale).
+int launch_amax(const void* x, int64_t numel, int in_code, float divisor, void* scale_out, uint32_t* partial,
+                hipStream_t st) {
     // torch's op-math reciprocal of the scalar divisor: fp32 division on the host
     const float inv_divisor = 1.0f / divisor;
     const int es = in_code == CKH_F32 ? 4 : 2;
     const bool vec = aligned(x, 16);
-    // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight
+    // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight; never
+    // more workgroups than the workspace has partial words
     const int64_t chunks = cdiv(numel * es, 16);
     const int blocks = static_cast<int>(
         std::max<int64_t>(1, std::min<int64_t>(am::kMaxBlocks, cdiv(chunks, am::kThreads * am::kUnroll))));
@@ -151,5 +151,90 @@ extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float d
     else if (in_code == CKH_F16) LAUNCH(CKH_F16);
     else LAUNCH(CKH_BF16);
 #undef LAUNCH
+    return CKH_OK;
+}
+
+int check_amax_args(const void* x, int64_t numel, int in_code, void* scale_out, const char* what) {
+    CKH_REQUIRE(x && scale_out, "%s: null pointer", what);
+    CKH_REQUIRE(numel > 0, "%s: empty tensor (torch.amax of an empty tensor is an error too)", what);
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "%s: unsupported input dtype code %d", what, in_code);
+    CKH_REQUIRE(aligned(scale_out, 4), "%s: scale_out misaligned", what);
+    return CKH_OK;
+}
+
+}  // namespace
+
+extern "C" int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
+                              void* workspace, uintptr_t stream) {
+    if (int rc = check_amax_args(x, numel, in_code, scale_out, "amax_scale")) return rc;
+    CKH_REQUIRE(workspace, "amax_scale: null pointer (workspace)");
+    CKH_REQUIRE(aligned(workspace, 4), "amax_scale: output or workspace misaligned");
+    launch_amax(x, numel, in_code, divisor, scale_out, static_cast<uint32_t*>(workspace),
+                reinterpret_cast<hipStream_t>(stream));
     return check_launch("amax_scale");
+}
+
+// ------------------------------------------------------------- no-allocation variant
+// The partial maxima of ckh_amax_scale_noalloc live in this file-scope device array
+// instead of a caller's workspace: CKH_AMAX_WORKSPACE_BYTES (8 KB) on each GPU the
+// library runs on, held until the process ends.  In host code `scratch` names a host-side
+// stand-in, not device memory: the kernels get the device address that
+// hipGetSymbolAddress returns for the current device, resolved once per device on the
+// first call there and cached.  Every call on a GPU shares that GPU's array, so calls
+// that overlap on one GPU (different streams, or threads) race on it.  Pass 2 reads only
+// the words pass 1 of the same call wrote, so nothing needs clearing between calls.
+static __device__ __align__(256) uint32_t scratch[am::kMaxBlocks];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<uint32_t*> g_scratch[kMaxDevices];  // device address of `scratch`, per device
+std::mutex g_scratch_init;
+
+// The device address of `scratch` on `dev`, which must be the current device.
+int scratch_on(int dev, uint32_t** out) {
+    uint32_t* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_init);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            void* addr = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || addr == nullptr) {
+                set_error("amax_scale_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                          hipGetErrorString(e));
+                return CKH_ERR_LAUNCH;
+            }
+            p = static_cast<uint32_t*>(addr);
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return CKH_OK;
+}
+
+}  // namespace
+
+extern "C" int ckh_amax_scale_noalloc(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
+                                      uintptr_t stream) {
+    if (int rc = check_amax_args(x, numel, in_code, scale_out, "amax_scale_noalloc")) return rc;
+    // The launch never uses more workgroups, i.e. partial words, than the scratch array
+    // holds (launch_amax caps the grid at kMaxBlocks), so no input size needs more of it.
+    static_assert(sizeof(scratch) == CKH_AMAX_WORKSPACE_BYTES, "scratch holds one word per workgroup");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int dev = -1, cur = -1;
+    hipError_t e = hipStreamGetDevice(st, &dev);
+    if (e == hipSuccess) e = hipGetDevice(&cur);
+    if (e != hipSuccess) {
+        set_error("amax_scale_noalloc: device query failed: %s", hipGetErrorString(e));
+        return CKH_ERR_LAUNCH;
+    }
+    CKH_REQUIRE(dev == cur, "amax_scale_noalloc: the stream belongs to device %d but device %d is current", dev, cur);
+    CKH_REQUIRE(dev >= 0 && dev < kMaxDevices, "amax_scale_noalloc: device %d beyond the %d supported", dev,
+                kMaxDevices);
+    uint32_t* partial = nullptr;
+    if (int rc = scratch_on(dev, &partial)) return rc;
+    launch_amax(x, numel, in_code, divisor, scale_out, partial, st);
+    return check_launch("amax_scale_noalloc");
 }

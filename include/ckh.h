@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 3
+#define CKH_ABI_VERSION 4
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -184,6 +184,20 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
 #define CKH_AMAX_WORKSPACE_BYTES 8192
 int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, void* scale_out,
                    void* workspace, uintptr_t stream);
+
+/*
+ * ckh_amax_scale without the workspace argument: the same kernels and result, with the
+ * per-workgroup partial maxima in an 8 KB (CKH_AMAX_WORKSPACE_BYTES) device array that
+ * the library holds on each GPU until the process ends.  The call allocates nothing
+ * (no hipMalloc, no torch allocator): for callers that cannot allocate, such as code
+ * under hipGraph capture with no allocator of its own or serving loops that forbid
+ * allocation.  Every input size fits (the grid never has more workgroups than the array
+ * has words).  `stream` must belong to the current device.  All calls on one GPU share
+ * its array: calls that overlap on that GPU (other streams, other threads) race and must
+ * be serialised by the caller.  No counterpart in the reference.
+ */
+int ckh_amax_scale_noalloc(const void* x, int64_t numel, int in_code, float divisor,
+                           void* scale_out, uintptr_t stream);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 3
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 4
 
 
 def test_amax_workspace_size_matches_header():
@@ -61,6 +61,13 @@ def test_invalid_arguments_return_error(lib):
     assert b"misaligned" in lib.ckh_last_error()
     assert f(p, 0, 2, 448.0, p, p, 0) == 1
     assert b"empty tensor" in lib.ckh_last_error()
+    g = lib.ckh_amax_scale_noalloc
+    assert g(p, 16, 2, 448.0, None, 0) == 1
+    assert b"null pointer" in lib.ckh_last_error()
+    assert g(p, 0, 2, 448.0, p, 0) == 1
+    assert b"empty tensor" in lib.ckh_last_error()
+    assert g(p, 16, 3, 448.0, p, 0) == 1
+    assert b"unsupported input dtype" in lib.ckh_last_error()
 
 
 def test_zero_sized_calls_are_noops(lib):
