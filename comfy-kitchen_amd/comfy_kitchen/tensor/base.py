@@ -1,18 +1,30 @@
-"""QuantizedTensor: a torch.Tensor subclass holding quantized storage plus typed layout
-parameters, with layout-specific handlers for the aten ops it intercepts.
+"""QuantizedTensor: a torch.Tensor subclass that presents a logical (dequantized) tensor
+while holding quantized storage plus a layout's typed parameters.
 
-Mirrors the reference's interface (tensor/base.py:1-511): the layout registry, the
-frozen `BaseLayoutParams` dataclass, the `QuantizedLayout` protocol, the
-`QuantizedTensor` wrapper subclass (`from_float`, `dequantize`, `state_dict`,
-`__tensor_flatten__` / `__tensor_unflatten__`), the generic handlers (detach, clone,
-to, _to_copy, contiguous, is_contiguous, copy_, empty_like), the per-layout handler
-table filled through `register_layout_op`, and the dequantize fallback for any other
-op.  The one deliberate difference: "fast matmul" support is decided by the device
-architecture (the hip backend's gfx950 kernels), not by a CUDA SM version.
+Interface kept from the reference (tensor/base.py:1-511), because checkpoints, layouts
+and callers depend on it: the layout registry (`register_layout_class`,
+`get_layout_class`), the frozen `BaseLayoutParams` dataclass with its `scale`,
+`orig_dtype`, `orig_shape` fields and `to_device` / `clone` / `copy_from`, the
+`QuantizedLayout` class methods (`quantize`, `dequantize`, `get_plain_tensors`,
+`state_dict_tensors`, `supports_fast_matmul`, `get_requirements`), the
+`QuantizedTensor(qdata, layout_name, params)` constructor with `_qdata`, `_layout_cls`,
+`_params`, `from_float`, `dequantize`, `state_dict`, the set of aten ops it intercepts,
+`register_layout_op`, and the dequantize fallback for every other op.
+
+Design of this implementation:
+  * Params rebuild themselves through one map over their tensor-valued fields (found by
+    value, so a layout adds tensor fields without listing them).
+  * Each layout class carries its own op table, filled by `register_layout_op`; a call
+    looks the op up along the layout's MRO, so a sub-layout inherits and may override.
+  * The layout-independent ops (detach, clone, to, _to_copy, contiguous, is_contiguous,
+    copy_, empty_like) are QuantizedTensor methods.  Their arguments are bound to names
+    through the aten op's schema, so every `to` overload reads the same `dtype` and
+    `device` names.
+  * "Fast matmul" support is decided by the device architecture (gfx950, where the hip
+    backend's GEMMs run), not by a CUDA SM version.
 """
 from __future__ import annotations
 
-import contextlib
 import dataclasses
 import logging
 from abc import ABC, abstractmethod
@@ -23,12 +35,14 @@ from typing import Any, Callable
 import torch
 
 logger = logging.getLogger(__name__)
+aten = torch.ops.aten
 
 # ----------------------------------------------------------------------------- layouts
 LAYOUTS: dict[str, type] = {}
 
 
 def register_layout_class(name: str, cls) -> None:
+    """Make layout class `cls` reachable by `name` (the string QuantizedTensors store)."""
     LAYOUTS[name] = cls
 
 
@@ -39,9 +53,7 @@ def get_layout_class(name: str):
 @lru_cache(maxsize=1)
 def get_cuda_capability() -> tuple[int, int] | None:
     """torch's device capability of the current GPU (on ROCm, gfx950 reports (9, 5))."""
-    if not torch.cuda.is_available():
-        return None
-    return torch.cuda.get_device_capability()
+    return torch.cuda.get_device_capability() if torch.cuda.is_available() else None
 
 
 @lru_cache(maxsize=1)
@@ -49,15 +61,16 @@ def get_device_arch() -> str | None:
     """gcnArchName of the current GPU, e.g. 'gfx950:sramecc+:xnack-'."""
     if not torch.cuda.is_available():
         return None
-    return getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", None)
+    props = torch.cuda.get_device_properties(torch.cuda.current_device())
+    return getattr(props, "gcnArchName", None)
 
 
 @dataclass(frozen=True)
 class BaseLayoutParams:
-    """Parameters shared by every layout: the scale tensor and the logical dtype/shape.
+    """Parameters every layout has: the scale tensor and the logical dtype / shape.
 
-    Subclasses add fields; `_tensor_fields` names every field holding a tensor so that
-    device moves, clones and in-place copies cover them all.
+    Layouts subclass it (as frozen dataclasses) to add fields.  Any field whose value is
+    a tensor travels with device moves, clones and in-place copies.
     """
 
     scale: torch.Tensor
@@ -68,35 +81,43 @@ class BaseLayoutParams:
         self._validate_tensor_fields()
 
     def _validate_tensor_fields(self):
-        pass
+        """Hook run after construction (and after every rebuild): normalise tensor fields."""
 
     def _tensor_fields(self) -> list[str]:
-        return ["scale"]
+        """Names of the fields holding tensors, in declaration order."""
+        return [f.name for f in dataclasses.fields(self) if isinstance(getattr(self, f.name), torch.Tensor)]
 
-    def _fields(self) -> dict[str, Any]:
-        return {f.name: getattr(self, f.name) for f in dataclasses.fields(self)}
+    def _map_tensors(self, fn: Callable[[torch.Tensor], torch.Tensor], **changes) -> BaseLayoutParams:
+        """A copy with fn applied to every tensor field and `changes` applied on top."""
+        new = {name: fn(getattr(self, name)) for name in self._tensor_fields()}
+        new.update(changes)
+        return dataclasses.replace(self, **new)
 
     def to_device(self, device: torch.device) -> BaseLayoutParams:
-        kw = self._fields()
-        for name in self._tensor_fields():
-            kw[name] = kw[name].to(device=device)
-        return type(self)(**kw)
+        return self._map_tensors(lambda t: t.to(device=device))
 
     def clone(self) -> BaseLayoutParams:
-        kw = self._fields()
-        for name in self._tensor_fields():
-            kw[name] = kw[name].clone()
-        return type(self)(**kw)
+        return self._map_tensors(torch.Tensor.clone)
 
     def copy_from(self, src: BaseLayoutParams, non_blocking: bool = False) -> None:
-        """Copy src's fields into self: tensors in place (reusing memory), others rebound."""
-        tensor_fields = set(self._tensor_fields())
+        """Take src's values in place: tensors are copied into this object's own tensors
+        (their memory is reused), every other field is rebound."""
+        tensors = set(self._tensor_fields())
         for f in dataclasses.fields(self):
             value = getattr(src, f.name)
-            if f.name in tensor_fields:
+            if f.name in tensors:
                 getattr(self, f.name).copy_(value, non_blocking=non_blocking)
             else:
                 object.__setattr__(self, f.name, value)
+
+
+def _op_table(layout_cls: type, create: bool = False) -> dict | None:
+    """The op table a layout class owns itself (not one inherited from a base)."""
+    table = layout_cls.__dict__.get("_layout_ops")
+    if table is None and create:
+        table = {}
+        setattr(layout_cls, "_layout_ops", table)
+    return table
 
 
 class QuantizedLayout(ABC):
@@ -130,14 +151,23 @@ class QuantizedLayout(ABC):
         raise NotImplementedError
 
     @classmethod
+    def handler_for(cls, op) -> Callable | None:
+        """The handler registered for aten `op` on this layout or the nearest base layout."""
+        for klass in cls.__mro__:
+            table = _op_table(klass)
+            if table and op in table:
+                return table[op]
+        return None
+
+    @classmethod
     def supports_fast_matmul(cls) -> bool:
         """True when the current GPU runs this layout's matmul on the hip kernels."""
         arch = get_device_arch()
-        if arch is None or not any(arch.startswith(a) for a in cls.REQUIRED_ARCH):
+        if arch is None or not arch.startswith(cls.REQUIRED_ARCH):
             return False
         from ..registry import registry
 
-        return bool(registry.list_backends().get("hip", {}).get("available", False))
+        return registry.is_available("hip")
 
     @classmethod
     def get_requirements(cls) -> dict[str, Any]:
@@ -151,10 +181,29 @@ class QuantizedLayout(ABC):
         }
 
 
+def register_layout_op(torch_op: Any, layout_cls: type[QuantizedLayout]):
+    """Decorator: `handler(qt, args, kwargs)` serves `torch_op` for QuantizedTensors of
+    `layout_cls` and of layouts derived from it (unless they register their own)."""
+
+    def decorator(handler):
+        _op_table(layout_cls, create=True)[torch_op] = handler
+        return handler
+
+    return decorator
+
+
+def _bind(func, args, kwargs) -> dict[str, Any]:
+    """An aten call's arguments by schema name (positional and keyword alike)."""
+    names = [a.name for a in func._schema.arguments]
+    bound = dict(zip(names, args))
+    bound.update(kwargs)
+    return bound
+
+
 # ----------------------------------------------------------------------------- tensor
 class QuantizedTensor(torch.Tensor):
-    """Quantized storage (`_qdata`) + layout name + typed params, presenting the logical
-    (unpadded) shape and the original dtype to torch.
+    """Quantized storage (`_qdata`) + layout name (`_layout_cls`) + typed params (`_params`),
+    presenting the logical (unpadded) shape and the original dtype to torch.
 
     `storage_shape` is the shape of the stored codes (padded, and for NVFP4 packed two
     per byte); `is_padded` tells whether the logical shape differs from the padded one.
@@ -192,10 +241,8 @@ class QuantizedTensor(torch.Tensor):
 
     @property
     def padded_shape(self) -> tuple[int, ...]:
-        layout = self.layout_cls
-        if hasattr(layout, "get_logical_shape_from_storage"):
-            return layout.get_logical_shape_from_storage(self.storage_shape)
-        return self.storage_shape
+        to_logical = getattr(self.layout_cls, "get_logical_shape_from_storage", None)
+        return to_logical(self.storage_shape) if to_logical else self.storage_shape
 
     @property
     def is_padded(self) -> bool:
@@ -215,13 +262,10 @@ class QuantizedTensor(torch.Tensor):
         qdata, params = get_layout_class(layout_cls).quantize(tensor, **kwargs)
         return cls(qdata, layout_cls, params)
 
-    def _copy_with(self, qdata: torch.Tensor | None = None, params: Any | None = None,
-                   clone_params: bool = True) -> QuantizedTensor:
-        if params is None:
-            params = self._params.clone() if clone_params else self._params
-        return QuantizedTensor(self._qdata if qdata is None else qdata, self._layout_cls, params)
+    def _rewrap(self, qdata: torch.Tensor, params: Any) -> QuantizedTensor:
+        return QuantizedTensor(qdata, self._layout_cls, params)
 
-    # ------------------------------------------------------------ core operations
+    # ------------------------------------------------------------ storage access
     def data_ptr(self):
         return self._qdata.data_ptr()
 
@@ -232,66 +276,124 @@ class QuantizedTensor(torch.Tensor):
         return self._qdata.storage()
 
     def dequantize(self) -> torch.Tensor:
-        """The logical tensor in orig_dtype (padding sliced off; deferred transposes applied)."""
-        qdata = self._qdata if self._qdata.is_contiguous() else self._qdata.contiguous()
-        full = self.layout_cls.dequantize(qdata, self._params)
-        shape = self._params.orig_shape
-        if getattr(self._params, "transposed", False):
-            physical = (shape[1], shape[0])
-            if tuple(full.shape[:2]) != physical:
-                full = full[: physical[0], : physical[1]]
-            return full.t()
-        if tuple(full.shape) != tuple(shape):
-            full = full[tuple(slice(0, s) for s in shape)]
-        return full
+        """The logical tensor in orig_dtype: padding cropped, a deferred transpose applied."""
+        full = self.layout_cls.dequantize(self._qdata.contiguous(), self._params)
+        rows_cols = tuple(self._params.orig_shape)
+        transposed = getattr(self._params, "transposed", False)
+        stored = rows_cols[::-1] if transposed else rows_cols
+        if tuple(full.shape) != stored:
+            full = full[tuple(slice(0, n) for n in stored)]
+        return full.t() if transposed else full
 
     def state_dict(self, prefix: str = "") -> dict[str, torch.Tensor]:
-        return {prefix + k: v for k, v in self.layout_cls.state_dict_tensors(self._qdata, self._params).items()}
+        tensors = self.layout_cls.state_dict_tensors(self._qdata, self._params)
+        return {f"{prefix}{suffix}": t for suffix, t in tensors.items()}
 
     # ------------------------------------------------------------ flatten protocol
+    # Inner tensors: the codes, then each tensor-valued param field under "_pt_<field>".
+    # The context holds the layout name, the params class, the tensor field names and
+    # the values of every other field.
     def __tensor_flatten__(self):
-        inner = ["_qdata"]
-        tensor_fields, other_fields = {}, {}
-        for f in dataclasses.fields(self._params):
-            value = getattr(self._params, f.name)
-            if isinstance(value, torch.Tensor):
-                attr = f"_param_{f.name}"
-                object.__setattr__(self, attr, value)
-                inner.append(attr)
-                tensor_fields[f.name] = attr
-            else:
-                other_fields[f.name] = value
-        return inner, {"layout_cls": self._layout_cls, "params_class": type(self._params),
-                       "tensor_fields": tensor_fields, "non_tensor_fields": other_fields}
+        tensor_fields = tuple(self._params._tensor_fields())
+        for name in tensor_fields:
+            object.__setattr__(self, f"_pt_{name}", getattr(self._params, name))
+        others = tuple((f.name, getattr(self._params, f.name)) for f in dataclasses.fields(self._params)
+                       if f.name not in tensor_fields)
+        ctx = (self._layout_cls, type(self._params), tensor_fields, others)
+        return ["_qdata", *(f"_pt_{n}" for n in tensor_fields)], ctx
 
     @staticmethod
     def __tensor_unflatten__(inner_tensors, ctx, outer_size, outer_stride):
-        kw = dict(ctx["non_tensor_fields"])
-        kw.update({name: inner_tensors[attr] for name, attr in ctx["tensor_fields"].items()})
-        return QuantizedTensor(inner_tensors["_qdata"], ctx["layout_cls"], ctx["params_class"](**kw))
+        layout_name, params_cls, tensor_fields, others = ctx
+        values = dict(others)
+        values.update({n: inner_tensors[f"_pt_{n}"] for n in tensor_fields})
+        return QuantizedTensor(inner_tensors["_qdata"], layout_name, params_cls(**values))
 
-    # ------------------------------------------------------------ dispatch
+    # ------------------------------------------------------------ generic ops
+    def _op_detach(self, a):
+        return self._rewrap(self._qdata.detach(), self._params._map_tensors(torch.Tensor.detach))
+
+    def _op_clone(self, a):
+        return self._rewrap(self._qdata.clone(), self._params.clone())
+
+    def _op_to(self, a, always_copy: bool = False):
+        device, dtype = a.get("device"), a.get("dtype")
+        device = torch.device(device) if isinstance(device, str) else device
+        move = device is not None and device != self._qdata.device
+        recast = dtype is not None and dtype != self._params.orig_dtype
+        if not (move or recast or always_copy):
+            return self
+        if move:
+            qdata, params = self._qdata.to(device=device), self._params.to_device(device)
+        else:
+            qdata, params = (self._qdata.clone() if always_copy else self._qdata), self._params.clone()
+        if recast:  # only the logical (dequantized) dtype changes; the codes stay
+            params = dataclasses.replace(params, orig_dtype=dtype)
+        return self._rewrap(qdata, params)
+
+    def _op_to_copy(self, a):
+        return self._op_to(a, always_copy=True)
+
+    def _op_contiguous(self, a):
+        return self if self._qdata.is_contiguous() else self._rewrap(self._qdata.contiguous(), self._params)
+
+    def _op_is_contiguous(self, a):
+        return self._qdata.is_contiguous()
+
+    def _op_copy_(self, a):
+        src = a["src"]
+        if not isinstance(src, QuantizedTensor):
+            raise TypeError(f"Cannot copy {type(src).__name__} to QuantizedTensor")
+        if src._layout_cls != self._layout_cls:
+            raise TypeError(f"Layout mismatch: {self._layout_cls} vs {src._layout_cls}")
+        non_blocking = bool(a.get("non_blocking", False))
+        keep = self._params.orig_dtype  # the destination keeps its logical dtype
+        self._qdata.copy_(src._qdata, non_blocking=non_blocking)
+        self._params.copy_from(src._params, non_blocking=non_blocking)
+        self._params = dataclasses.replace(self._params, orig_dtype=keep)
+        return self
+
+    def _op_empty_like(self, a):
+        device, dtype = a.get("device"), a.get("dtype")
+        params = self._params.clone() if device is None else self._params.to_device(device)
+        if dtype is not None:
+            params = dataclasses.replace(params, orig_dtype=dtype)
+        return self._rewrap(torch.empty_like(self._qdata, device=device), params)
+
+    def _op_shallow_copy_ok(self, a):
+        return True
+
     @classmethod
     def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
         kwargs = kwargs or {}
-        qt = args[0] if args else None
-        generic = _GENERIC_HANDLERS.get(func)
-        if generic is not None:
-            return generic(qt, args, kwargs)
-        layout = _layout_of(args)
-        if layout is not None:
-            per_layout = _LAYOUT_HANDLERS.get(func)
-            if per_layout:
-                for klass in layout.__mro__:
-                    handler = per_layout.get(klass)
-                    if handler is not None:
-                        return handler(qt, args, kwargs)
-        logger.debug("unhandled %s for %s: dequantizing", func, layout.__name__ if layout else "?")
+        method = _GENERIC_OPS.get(func)
+        if method is not None and args and isinstance(args[0], QuantizedTensor):
+            return getattr(args[0], method)(_bind(func, args, kwargs))
+        layout = _first_layout(args)
+        handler = layout.handler_for(func) if layout is not None else None
+        if handler is not None:
+            return handler(args[0] if args else None, args, kwargs)
+        logger.debug("%s has no handler for %s: dequantizing", getattr(layout, "__name__", "?"), func)
         return func(*dequantize_args(args), **dequantize_args(kwargs))
 
 
+_GENERIC_OPS: dict[Any, str] = {
+    aten.detach.default: "_op_detach",
+    aten.clone.default: "_op_clone",
+    aten.to.dtype_layout: "_op_to",
+    aten.to.dtype: "_op_to",
+    aten.to.device: "_op_to",
+    aten._to_copy.default: "_op_to_copy",
+    aten.contiguous.default: "_op_contiguous",
+    aten.is_contiguous.default: "_op_is_contiguous",
+    aten.copy_.default: "_op_copy_",
+    aten.empty_like.default: "_op_empty_like",
+    aten._has_compatible_shallow_copy_type.default: "_op_shallow_copy_ok",
+}
+
+
 def dequantize_args(args):
-    """Replace every QuantizedTensor inside (nested) args by its dequantized tensor."""
+    """`args` with every QuantizedTensor inside (nested lists, tuples, dicts) dequantized."""
     if isinstance(args, QuantizedTensor):
         return args.dequantize()
     if isinstance(args, dict):
@@ -301,101 +403,13 @@ def dequantize_args(args):
     return args
 
 
-def _layout_of(args) -> type[QuantizedLayout] | None:
+def _first_layout(args) -> type[QuantizedLayout] | None:
+    """Layout class of the first QuantizedTensor among args (one level of nesting)."""
     for a in args:
-        if isinstance(a, QuantizedTensor):
-            return get_layout_class(a._layout_cls)
-        if isinstance(a, (list, tuple)):
-            for b in a:
-                if isinstance(b, QuantizedTensor):
-                    return get_layout_class(b._layout_cls)
+        for t in (a if isinstance(a, (list, tuple)) else (a,)):
+            if isinstance(t, QuantizedTensor):
+                return get_layout_class(t._layout_cls)
     return None
-
-
-# ----------------------------------------------------------------------------- generic handlers
-def _to_target(args, kwargs) -> tuple[torch.device | None, torch.dtype | None]:
-    """(device, dtype) requested by a .to(...) call's positional and keyword arguments."""
-    device, dtype = kwargs.get("device"), kwargs.get("dtype")
-    for a in args[1:]:
-        if isinstance(a, torch.device):
-            device = a
-        elif isinstance(a, torch.dtype):
-            dtype = a
-        elif isinstance(a, str):
-            with contextlib.suppress(RuntimeError, ValueError):
-                device = torch.device(a)
-    if isinstance(device, str):
-        device = torch.device(device)
-    return device, dtype
-
-
-def _to(qt: QuantizedTensor, args, kwargs, force_copy: bool = False):
-    device, dtype = _to_target(args, kwargs)
-    move = device is not None and device != qt._qdata.device
-    recast = dtype is not None and dtype != qt._params.orig_dtype
-    if not (move or recast or force_copy):
-        return qt
-    if move:
-        qdata, params = qt._qdata.to(device=device), qt._params.to_device(device)
-    else:
-        qdata, params = (qt._qdata.clone() if force_copy else qt._qdata), qt._params.clone()
-    if recast:  # the codes stay; only the logical (dequantized) dtype changes
-        params = dataclasses.replace(params, orig_dtype=dtype)
-    return qt._copy_with(qdata=qdata, params=params, clone_params=False)
-
-
-def _copy_(qt, args, kwargs):
-    dst, src = args[0], args[1]
-    if not isinstance(src, QuantizedTensor):
-        raise TypeError(f"Cannot copy {type(src).__name__} to QuantizedTensor")
-    if dst._layout_cls != src._layout_cls:
-        raise TypeError(f"Layout mismatch: {dst._layout_cls} vs {src._layout_cls}")
-    keep_dtype = dst._params.orig_dtype
-    non_blocking = kwargs.get("non_blocking", len(args) >= 3)
-    dst._qdata.copy_(src._qdata, non_blocking=non_blocking)
-    dst._params.copy_from(src._params, non_blocking=non_blocking)
-    dst._params = dataclasses.replace(dst._params, orig_dtype=keep_dtype)
-    return dst
-
-
-def _empty_like(qt, args, kwargs):
-    dtype = kwargs.pop("dtype", None)
-    device = kwargs.get("device")
-    params = qt._params.clone()
-    if device is not None:
-        params = params.to_device(device)
-    if dtype is not None:
-        params = dataclasses.replace(params, orig_dtype=dtype)
-    return qt._copy_with(qdata=torch.empty_like(qt._qdata, device=device), params=params, clone_params=False)
-
-
-aten = torch.ops.aten
-_GENERIC_HANDLERS: dict[Any, Callable] = {
-    aten.detach.default: lambda qt, a, k: qt._copy_with(qdata=qt._qdata.detach()),
-    aten.clone.default: lambda qt, a, k: qt._copy_with(qdata=qt._qdata.clone()),
-    aten._to_copy.default: lambda qt, a, k: _to(qt, a, k, force_copy=True),
-    aten.to.dtype_layout: _to,
-    aten.to.dtype: _to,
-    aten.contiguous.default: lambda qt, a, k: qt if qt._qdata.is_contiguous()
-    else qt._copy_with(qdata=qt._qdata.contiguous()),
-    aten.is_contiguous.default: lambda qt, a, k: qt._qdata.is_contiguous(),
-    aten.copy_.default: _copy_,
-    aten.empty_like.default: _empty_like,
-    aten._has_compatible_shallow_copy_type.default: lambda qt, a, k: True,
-}
-
-# {aten op: {layout class: handler(qt, args, kwargs)}}
-_LAYOUT_HANDLERS: dict[Any, dict[type, Callable]] = {}
-
-
-def register_layout_op(torch_op: Any, layout_cls: type[QuantizedLayout]):
-    """Decorator: handle `torch_op` for QuantizedTensors of `layout_cls` (and subclasses)."""
-
-    def decorator(handler):
-        _LAYOUT_HANDLERS.setdefault(torch_op, {})[layout_cls] = handler
-        return handler
-
-    return decorator
 
 
 def slice_to(result: torch.Tensor, rows: int, cols: int) -> torch.Tensor:

@@ -37,9 +37,6 @@ class TensorCoreNVFP4Layout(QuantizedLayout):
         block_scale: torch.Tensor
         transposed: bool = False
 
-        def _tensor_fields(self) -> list[str]:
-            return ["scale", "block_scale"]
-
         def _validate_tensor_fields(self):
             if isinstance(self.scale, torch.Tensor) and self.scale.dtype != torch.float32:
                 object.__setattr__(self, "scale", self.scale.to(dtype=torch.float32, non_blocking=True))
