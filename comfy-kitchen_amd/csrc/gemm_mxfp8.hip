@@ -23,9 +23,12 @@
 // Pipeline: at stage t (after its barrier) the fragments of t are already in
 // registers; the LDS reads of stage t+1's fragments and scale words overlap stage t's
 // 16 MFMAs.  Global data moves in pairs of stages through registers: one load
-// instruction brings whole 128-byte lines (both stages' halves of 8 rows), and an even
-// stage t writes the staged pair t+2, t+3 to LDS and loads t+4, t+5, so loads have two
-// stages (~2000 MFMA cycles) to arrive.  Register staging rather than direct-to-LDS
+// instruction brings whole 128-byte lines (both stages' halves of 8 rows).  An even
+// stage t writes the staged weight pair t+2, t+3 to LDS and loads the activation pair
+// t+4, t+5; the odd stage after it writes that pair and loads the next weight pair, so
+// each load has one stage (~1000 MFMA cycles) to arrive.  (Keeping each operand's
+// registers for two stages instead makes both staged sets loop-carried, and the
+// compiler then drains every load each stage.)  Register staging rather than direct-to-LDS
 // loads because each buffer_load ... lds instruction holds up the issuing wave's MFMA
 // stream for ~22 cycles on gfx950, while plain loads and ds_writes hide under the MFMAs.
 // Each barrier waits for LDS traffic only; the compiler's vmcnt waits guard the staged
@@ -37,9 +40,9 @@
 // Workgroups are dispatched round-robin over the 8 XCDs; the tile index is remapped
 // so each XCD walks a contiguous range of tiles in grouped order (grouped_tile), so the
 // tiles an XCD runs at once share few operand panels in its L2.  Tiles run one per CU
-// in rounds; when the
-// last round would be at most half full, its tiles go to a second launch as 256 x 128
-// half tiles (2 MFMA columns per wave, 8-slot stages) on twice as many CUs.
+// in rounds; when the last round would be at most half full, its tiles run as 256 x 128
+// half tiles (2 MFMA columns per wave, 8-slot stages) on twice as many CUs, in the same
+// grid after the full tiles.
 #include <type_traits>
 #include <utility>
 
@@ -51,6 +54,9 @@ namespace mx {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
 constexpr int TILE = 256 * BK;  // bytes of one operand tile per stage (16 KB)
@@ -60,7 +66,7 @@ constexpr int STILE = 1024;     // bytes of one operand's scale words per stage 
 // from 8 neighbouring lanes (64 bytes each), which the padding puts in opposite halves
 // of the bank cycle (measured conflict-free; without it every store conflicts 2-way).
 constexpr int BUF = 2 * TILE + 2 * STILE + 64;
-constexpr int EPI_ROW = 520;  // bytes of one staged 16-bit output row (512 + 8 pad)
+constexpr int EPI_ROW = 528;  // bytes of one staged 16-bit output row (512 + 16 pad, rows 16-byte aligned)
 static_assert(64 * EPI_ROW <= BUF, "an output slab must fit one stage buffer");
 
 // s_waitcnt immediates (gfx9 encoding): vmcnt in [3:0] and [15:14], expcnt [6:4],
@@ -269,6 +275,20 @@ __device__ __forceinline__ void store4(void* out, int64_t idx, const float (&v)[
     }
 }
 
+// Two floats to two 16-bit values (RNE) in one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, low
+// half first.  `opaque` keeps an fp32 product or sum feeding the convert from being fused
+// into a single-rounding mixed-precision instruction.
+template <int OUT, bool HIDE>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    if constexpr (HIDE) {
+        a = opaque(a);
+        b = opaque(b);
+    }
+    const v2f v = {a, b};
+    if constexpr (OUT == CKH_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2bf));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, v2h));
+}
+
 template <int OUT>
 __device__ __forceinline__ void store1(void* out, int64_t idx, float v) {
     if constexpr (OUT == CKH_F32) static_cast<float*>(out)[idx] = v;
@@ -442,14 +462,22 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     using B2 = std::integral_constant<int, 2>;
     using B3 = std::integral_constant<int, 3>;
 
-    // prologue: stages 0..3 resident except the weight half of 2, 3 (staged), stage 0 read
-    load_a(0);
-    load_b(0);
-    store_a(B0{}, B1{});
-    load_a(2);
-    store_b(B0{}, B1{});
-    load_b(2);
-    store_a(B2{}, B3{});
+    // prologue: stages 0..3 resident except the weight half of 2, 3 (staged in SB for
+    // stage 0 to write), stage 0 read.  All four pairs are loaded before the first LDS
+    // write, so the prologue waits out one memory latency rather than two.
+    {
+        v4u XA[8], XB[8];
+        ScaleWords XW;
+        load_a(0);
+        load_pair<PB>(LB, XB, 0, p.K);
+        if constexpr (!UNIT) load_scales(XW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, 0, p.K, wave, lane);
+        load_pair(LA, XA, 2 * BK, p.K);
+        load_b(2);
+        store_a(B0{}, B1{});
+        store_pair<PB>(LB, XB, buf(B0{}), buf(B1{}));
+        if constexpr (!UNIT) store_scales(XW, buf(B0{}) + 2 * TILE, buf(B1{}) + 2 * TILE, wave, lane);
+        store_pair(LA, XA, buf(B2{}) + TILE, buf(B3{}) + TILE);
+    }
     stage_barrier<WAIT_LGKM0>();
     read_frags(F0, lds01, fab, faa);
     read_scales(B0{}, scb, sca);
@@ -467,15 +495,18 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
     // n = 8*g + 4*half (+0..3) of weight tile i.
     const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
+    // With neither a tensor scale nor a bias the accumulator is the output value.
+    constexpr bool ARITH = UNIT || BIAS >= 0;
     auto value = [&](float a, int n) {
         if constexpr (UNIT) a *= alpha;
-        return a + (n < p.N ? bias_at<BIAS>(p.bias, n) : 0.0f);
+        if constexpr (BIAS >= 0) a += n < p.N ? bias_at<BIAS>(p.bias, n) : 0.0f;
+        return a;
     };
     if constexpr (OUT != CKH_F32) {
         // 16-bit output: stage the tile in LDS as 256 rows of 512 bytes, the 64-row slab
-        // q in buffer q.  The pitch EPI_ROW = 520 spreads the 32 rows of one fragment
-        // store over distinct bank pairs.  Then each wave stores whole rows of its slab:
-        // 64 lanes x 8 bytes per row.
+        // q in buffer q, converting two values per instruction.  Then each wave stores
+        // whole rows of its slab, 16 bytes per lane: two 512-byte rows per instruction
+        // (NW = 4) or four 256-byte rows (NW = 2).
         auto slab = [&](int q) -> uint8_t* { return (q < 2 ? lds01 : lds23) + (q & 1) * BUF; };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -486,38 +517,33 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
                 for (int g = 0; g < 4; ++g) {
                     const int nl = wn * 32 * NW + i * 32 + 8 * g + 4 * half;
                     const int n = n0 + nl;
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * g + e], n + e);
-                    uint32_t w0 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[0]) : f_to_f16(v[0])) |
-                                  ((OUT == CKH_BF16 ? f_to_bf16_rne(v[1]) : f_to_f16(v[1])) << 16);
-                    uint32_t w1 = (OUT == CKH_BF16 ? f_to_bf16_rne(v[2]) : f_to_f16(v[2])) |
-                                  ((OUT == CKH_BF16 ? f_to_bf16_rne(v[3]) : f_to_f16(v[3])) << 16);
+                    const v16f& a = acc[i][j];
+                    const uint32_t w0 = pack2<OUT, ARITH>(value(a[4 * g], n), value(a[4 * g + 1], n + 1));
+                    const uint32_t w1 = pack2<OUT, ARITH>(value(a[4 * g + 2], n + 2), value(a[4 * g + 3], n + 3));
                     *reinterpret_cast<uint2*>(rowp + nl * 2) = make_uint2(w0, w1);
                 }
             }
         }
         __syncthreads();
-        // a row of the tile is TBN * 2 bytes: 64 lanes x 8 bytes (NW = 4) or 32 lanes x 8
-        // bytes with the wave's two halves on consecutive rows (NW = 2)
-        constexpr int LPR = TBN / 4;  // lanes per output row
+        constexpr int LPR = TBN / 8;  // lanes per output row, 16 bytes (8 values) each
+        constexpr int RPI = 64 / LPR;  // rows per store instruction
         const int lr = lane % LPR, lrow = lane / LPR;
-        const uint8_t* src = slab(wave) + lrow * EPI_ROW + lr * 8;
-        const int n = n0 + 4 * lr;
-        const bool vec = (p.N & 3) == 0 && n + 4 <= p.N;
+        const uint8_t* src = slab(wave) + lrow * EPI_ROW + lr * 16;
+        const int n = n0 + 8 * lr;
+        const bool vec = (p.N & 7) == 0 && n + 8 <= p.N;
         uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64 + lrow) * p.N + n;
         const int rows = min(64, p.M - (m0 + wave * 64)) - lrow;
 #pragma unroll 8
-        for (int rl = 0; rl < 64; rl += 64 / LPR) {
-            const uint2 d = *reinterpret_cast<const uint2*>(src + rl * EPI_ROW);
+        for (int rl = 0; rl < 64; rl += RPI) {
+            const v4u d = *reinterpret_cast<const v4u*>(src + rl * EPI_ROW);
             if (rl >= rows) break;
             uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
             if (vec) {
-                *reinterpret_cast<uint2*>(o) = d;
+                *reinterpret_cast<v4u*>(o) = d;
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (n + e < p.N) o[e] = static_cast<uint16_t>((e < 2 ? d.x : d.y) >> (16 * (e & 1)));
+                for (int e = 0; e < 8; ++e)
+                    if (n + e < p.N) o[e] = static_cast<uint16_t>(d[e >> 1] >> (16 * (e & 1)));
             }
         }
     } else {
