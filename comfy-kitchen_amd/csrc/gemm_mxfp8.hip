@@ -360,10 +360,6 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
-    auto store_b = [&](auto x_c, auto y_c) {
-        store_pair<PB>(LB, SB, buf(x_c), buf(y_c));
-        if constexpr (!UNIT) store_scales(SW, buf(x_c) + 2 * TILE, buf(y_c) + 2 * TILE, wave, lane);
-    };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
