@@ -118,6 +118,18 @@ FLOPS = {
     "scaled_mm_mxfp8": 2 * 4608 * 12288 * 3072,
     "scaled_mm_nvfp4": 2 * 8192 * 13824 * 5120,
 }
+# (bytes read, bytes written) per call of each streaming op: the copy floor moves the same.
+READ_WRITE = {
+    "quantize_per_tensor_fp8": (4096 * 3072 * 2 + 4, 4096 * 3072),
+    "dequantize_per_tensor_fp8": (4096 * 3072 + 4, 4096 * 3072 * 2),
+    "apply_rope": (2 * 24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4, 2 * 24 * 4608 * 128 * 2),
+    "apply_rope1": (24 * 4608 * 128 * 2 + 4608 * 64 * 4 * 4, 24 * 4608 * 128 * 2),
+    "quantize_mxfp8": (4608 * 3072 * 2, 4608 * 3072 + 4608 * 96),
+    "dequantize_mxfp8": (4608 * 3072 + 4608 * 96, 4608 * 3072 * 2),
+    "quantize_nvfp4": (8192 * 5120 * 2 + 4, 8192 * 2560 + 8192 * 320),
+    "dequantize_nvfp4": (8192 * 2560 + 8192 * 320 + 4, 8192 * 5120 * 2),
+}
+assert all(r + w == BYTES[k] for k, (r, w) in READ_WRITE.items())
 
 
 # ------------------------------------------------------------------ timing
@@ -180,6 +192,53 @@ def time_cpu(fn, min_reps=3, budget_s=3.0) -> tuple[float, int]:
     return ts[len(ts) // 2], len(ts)
 
 
+_bench_lib = None
+
+
+def bench_lib():
+    """comfy-kitchen_amd/benchlib/libckh_bench.so: kernels timed only for comparison."""
+    global _bench_lib
+    if _bench_lib is None:
+        import ctypes
+
+        lib = ctypes.CDLL(str(REPO / "comfy-kitchen_amd" / "benchlib" / "libckh_bench.so"))
+        lib.ckh_bench_copy_floor.restype = ctypes.c_int
+        lib.ckh_bench_copy_floor.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
+                                             ctypes.c_uint64]
+        _bench_lib = lib
+    return _bench_lib
+
+
+def copy_floor_ms(read_bytes: int, write_bytes: int, steps: int, warmup: int) -> float:
+    """Per-call time of a streaming copy that reads and writes the given bytes, timed like the
+    ops: a HIP graph of `steps` calls over buffer sets rotating through > 512 MB."""
+    lib = bench_lib()
+    dev = torch.device("cuda", 0)
+    nset = _sets_for(read_bytes + write_bytes)
+    srcs = [torch.randint(0, 255, (read_bytes,), dtype=torch.uint8, device=dev) for _ in range(nset)]
+    dsts = [torch.empty(write_bytes, dtype=torch.uint8, device=dev) for _ in range(nset)]
+
+    def make(i):
+        def call():
+            st = torch.cuda.current_stream().cuda_stream
+            if lib.ckh_bench_copy_floor(srcs[i].data_ptr(), read_bytes, dsts[i].data_ptr(), write_bytes, st):
+                raise RuntimeError("copy floor launch failed")
+            return dsts[i]
+        return call
+
+    ms = time_graph(make, nset, steps, warmup)
+    del srcs, dsts
+    return ms
+
+
+def add_copy_floor(res: dict, name: str, steps: int, warmup: int, log) -> None:
+    r, w = READ_WRITE[name]
+    floor = copy_floor_ms(r, w, steps, warmup)
+    res[name]["copy_floor_ms"] = floor
+    res[name]["of_copy_floor"] = round(floor / res[name]["ms"], 4)
+    log(f"   copy floor for {name}'s bytes: {floor * 1e3:.2f} us ({res[name]['of_copy_floor'] * 100:.1f}% of it)")
+
+
 def roofline_bytes(nbytes, ms, traffic=None):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -226,6 +285,7 @@ def run_gpu(configs, steps, warmup, log):
         res["quantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_per_tensor_fp8"], ms,
                                                                       traffic.get("quantize_per_tensor_fp8"))}
         log(f"c1 quantize_per_tensor_fp8: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "quantize_per_tensor_fp8", steps, warmup, log)
         qs = [ref_q.clone() for _ in range(nset)]
         ref_dq = ck.dequantize_per_tensor_fp8(ref_q, scale)
         ms = time_graph(lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
@@ -233,6 +293,7 @@ def run_gpu(configs, steps, warmup, log):
         res["dequantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_per_tensor_fp8"], ms,
                                                                         traffic.get("dequantize_per_tensor_fp8"))}
         log(f"c1 dequantize_per_tensor_fp8: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "dequantize_per_tensor_fp8", steps, warmup, log)
         del xs, qs
 
     if "c2" in configs:
@@ -245,11 +306,13 @@ def run_gpu(configs, steps, warmup, log):
                         check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
         res["apply_rope"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope"], ms, traffic.get("apply_rope"))}
         log(f"c2 apply_rope: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "apply_rope", steps, warmup, log)
         rq1 = ck.apply_rope1(q, f)
         ms = time_graph(lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
                         check=lambda outs: [same(o, rq1) or sys.exit("graph mismatch c2 rope1") for o in outs])
         res["apply_rope1"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope1"], ms, traffic.get("apply_rope1"))}
         log(f"c2 apply_rope1: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "apply_rope1", steps, warmup, log)
         del qs, ks
 
     if "c3" in configs or "c4" in configs:
@@ -264,6 +327,7 @@ def run_gpu(configs, steps, warmup, log):
             res["quantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_mxfp8"], ms,
                                                                  traffic.get("quantize_mxfp8"))}
             log(f"c3 quantize_mxfp8: {ms * 1e3:.2f} us")
+            add_copy_floor(res, "quantize_mxfp8", steps, warmup, log)
             del xs
             # the layouts' dequantize of the same tensor (bf16 out)
             want = ck.dequantize_mxfp8(qa, sa)
@@ -275,6 +339,7 @@ def run_gpu(configs, steps, warmup, log):
             res["dequantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_mxfp8"], ms,
                                                                    traffic.get("dequantize_mxfp8"))}
             log(f"c3 dequantize_mxfp8: {ms * 1e3:.2f} us")
+            add_copy_floor(res, "dequantize_mxfp8", steps, warmup, log)
             del qs_, want
         if "c4" in configs:
             qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
@@ -302,6 +367,26 @@ def run_gpu(configs, steps, warmup, log):
                                             for x_, y_ in outs])
         res["quantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["quantize_nvfp4"], ms, traffic.get("quantize_nvfp4"))}
         log(f"c5 quantize_nvfp4: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "quantize_nvfp4", steps, warmup, log)
+        # dynamic scale (the layouts' scale=None): the fused call against amax_scale + quantize
+        g_dyn = ck.amax_scale(a, 2688.0)
+        q_dyn, s_dyn = ck.quantize_nvfp4(a, g_dyn)
+
+        def check_dyn(outs):
+            for o in outs:
+                q_, s_, g_ = o if len(o) == 3 else (*o, None)
+                if not (same(q_, q_dyn) and same(s_, s_dyn)) or (g_ is not None and not torch.equal(g_, g_dyn)):
+                    sys.exit("graph mismatch c5 dynamic")
+
+        ms_fused = time_graph(lambda i: (lambda: ck.quantize_nvfp4_dynamic(as_[i], 2688.0)), nset, steps, warmup,
+                              check=check_dyn)
+        ms_two = time_graph(lambda i: (lambda: ck.quantize_nvfp4(as_[i], ck.amax_scale(as_[i], 2688.0))), nset,
+                            steps, warmup, check=check_dyn)
+        res["quantize_nvfp4_dynamic"] = {
+            "ms": ms_fused, **roofline_bytes(BYTES["quantize_nvfp4"], ms_fused),
+            "two_call_ms": ms_two, "note": "amax(|x|)/2688 + quantize_nvfp4 in two launches (x re-read from the "
+                                           "infinity cache) vs amax_scale (2 launches) + quantize_nvfp4"}
+        log(f"c5 quantize_nvfp4_dynamic: {ms_fused * 1e3:.2f} us fused vs {ms_two * 1e3:.2f} us amax_scale + quantize")
         del as_
         want = ck.dequantize_nvfp4(qa, ga, sa)
         nset = _sets_for(BYTES["dequantize_nvfp4"])
@@ -311,6 +396,7 @@ def run_gpu(configs, steps, warmup, log):
         res["dequantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_nvfp4"], ms,
                                                                traffic.get("dequantize_nvfp4"))}
         log(f"c5 dequantize_nvfp4: {ms * 1e3:.2f} us")
+        add_copy_floor(res, "dequantize_nvfp4", steps, warmup, log)
         del qs_, want
         qw, sw = ck.quantize_nvfp4(w, gw)
         try:
@@ -331,48 +417,84 @@ def run_gpu(configs, steps, warmup, log):
     return res
 
 
+def host_info() -> dict:
+    """CPU model, logical CPU count and torch version of this host."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "torch": torch.__version__}
+
+
 def run_cpu_baseline(configs, log):
-    """Time the CPU oracle (restatement of the reference eager path) on bounded samples."""
+    """Time the CPU oracle (restatement of the reference eager path) on bounded samples.
+
+    Threads: the host share of a one-GPU box, OMP_NUM_THREADS (16 there), rather than
+    os.cpu_count(), which counts every CPU of a host shared by several GPU boxes; both are
+    recorded with each figure."""
     from oracle import eager_ref as ref
 
-    # the host share of a one-GPU box is OMP_NUM_THREADS cores, not os.cpu_count()
     torch.set_num_threads(int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1))
     cores = torch.get_num_threads()
+    host = host_info()
     out = {}
+
+    def put(name, value, unit, sample):
+        out[name] = {"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample, **host}
+        log(f"cpu {name}: {value} {unit} ({sample})")
+
+    def gbs(name, nbytes, fn, sample, **kw):
+        s, reps = time_cpu(fn, **kw)
+        put(name, round(nbytes / s / 1e9, 3), "GB/s", f"{sample}, median of {reps} runs")
+
     if "c3" in configs:
         x = make_c3()
-        s, reps = time_cpu(lambda: ref.quantize_mxfp8(x), budget_s=12.0)
-        out["quantize_mxfp8"] = {"value": round(BYTES["quantize_mxfp8"] / s / 1e9, 3), "unit": "GB/s",
-                                 "cores": cores, "kind": "port",
-                                 "sample": f"full C3 tensor [4608, 3072] bf16, median of {reps} runs (~12 s of CPU work)"}
-        log(f"cpu quantize_mxfp8: {s * 1e3:.1f} ms")
+        gbs("quantize_mxfp8", BYTES["quantize_mxfp8"], lambda: ref.quantize_mxfp8(x),
+            "full C3 tensor [4608, 3072] bf16 (~12 s of CPU work)", budget_s=12.0)
+        q, sc = ref.quantize_mxfp8(x)
+        gbs("dequantize_mxfp8", BYTES["dequantize_mxfp8"], lambda: ref.dequantize_mxfp8(q, sc, torch.bfloat16),
+            "full C3 codes and scales, bf16 out")
     if "c1" in configs:
         x, scale = make_c1()
-        s, reps = time_cpu(lambda: ref.quantize_per_tensor_fp8(x, scale))
-        out["quantize_per_tensor_fp8"] = {"value": round(BYTES["quantize_per_tensor_fp8"] / s / 1e9, 3),
-                                          "unit": "GB/s", "cores": cores, "kind": "port",
-                                          "sample": f"full C1 tensor, median of {reps} runs"}
+        gbs("quantize_per_tensor_fp8", BYTES["quantize_per_tensor_fp8"],
+            lambda: ref.quantize_per_tensor_fp8(x, scale), "full C1 tensor")
+        q = ref.quantize_per_tensor_fp8(x, scale)
+        gbs("dequantize_per_tensor_fp8", BYTES["dequantize_per_tensor_fp8"],
+            lambda: ref.dequantize_per_tensor_fp8(q, scale, torch.bfloat16), "full C1 codes, bf16 out")
     if "c2" in configs:
         q, k, f = make_c2()
-        s, reps = time_cpu(lambda: ref.apply_rope(q, k, f))
-        out["apply_rope"] = {"value": round(BYTES["apply_rope"] / s / 1e9, 3), "unit": "GB/s", "cores": cores,
-                             "kind": "port", "sample": f"full C2 q,k, median of {reps} runs"}
+        gbs("apply_rope", BYTES["apply_rope"], lambda: ref.apply_rope(q, k, f), "full C2 q, k")
+        gbs("apply_rope1", BYTES["apply_rope1"], lambda: ref.apply_rope1(q, f), "full C2 q")
     if "c5" in configs:
-        a = make_c5()[0][:1024]
+        a_full, w_full, _, _ = make_c5()
+        a = a_full[:1024]
         ga = (a.abs().amax().float() / 2688).reshape(1)
-        s, reps = time_cpu(lambda: ref.quantize_nvfp4(a, ga))
-        out["quantize_nvfp4"] = {"value": round(BYTES["quantize_nvfp4"] / 8 / s / 1e9, 3), "unit": "GB/s",
-                                 "cores": cores, "kind": "port",
-                                 "sample": f"first 1024 of 8192 rows of C5 A, median of {reps} runs"}
-    if "c4" in configs:
+        gbs("quantize_nvfp4", BYTES["quantize_nvfp4"] // 8, lambda: ref.quantize_nvfp4(a, ga),
+            "first 1024 of 8192 rows of C5 A")
+        qa, sa = ref.quantize_nvfp4(a, ga)
+        gbs("dequantize_nvfp4", BYTES["dequantize_nvfp4"] // 8,
+            lambda: ref.dequantize_nvfp4(qa, ga, sa, torch.bfloat16), "first 1024 of 8192 rows of C5 A, bf16 out")
         # eager scaled_mm has no CPU kernel; stand-in: dequantize both operands, fp32 matmul
+        w = w_full[:1024]
+        gw = (w.abs().amax().float() / 2688).reshape(1)
+        qw, sw = ref.quantize_nvfp4(w, gw)
+        qa2, sa2 = qa[:256].contiguous(), ref.to_blocked(ref.from_blocked(sa, 1024, 320)[:256].contiguous())
+        s, reps = time_cpu(lambda: ref.scaled_mm_nvfp4_ref(qa2, qw, ga, gw, sa2, sw), min_reps=1, budget_s=5.0)
+        put("scaled_mm_nvfp4", round(2 * 256 * 1024 * 5120 / s / 1e12, 4), "TFLOP/s",
+            f"256 of 8192 rows of A x 1024 of 13824 rows of W: dequantize both + fp32 matmul, median of {reps}")
+        del a_full, w_full
+    if "c4" in configs:
         x = make_c3()[:512]
         wq, ws = ref.quantize_mxfp8(make_c4_weight())
         xq, xs = ref.quantize_mxfp8(x)
         s, reps = time_cpu(lambda: ref.scaled_mm_mxfp8_ref(xq, wq, xs, ws), min_reps=1, budget_s=5.0)
-        out["scaled_mm_mxfp8"] = {"value": round(2 * 512 * 12288 * 3072 / s / 1e12, 4), "unit": "TFLOP/s",
-                                  "cores": cores, "kind": "port",
-                                  "sample": f"512 of 4608 rows of A: dequantize + fp32 matmul, median of {reps}"}
+        put("scaled_mm_mxfp8", round(2 * 512 * 12288 * 3072 / s / 1e12, 4), "TFLOP/s",
+            f"512 of 4608 rows of A: dequantize both + fp32 matmul, median of {reps}")
     return out
 
 

@@ -4,6 +4,8 @@
 
 Every csrc/*.hip file is compiled by hipcc for gfx950 only and linked into
 comfy_kitchen/backends/hip/libckh.so, which the "hip" backend loads with ctypes.
+benchlib/*.hip (kernels bench.py times for comparison, e.g. the copy floor) is linked
+into benchlib/libckh_bench.so, separate from the product library.
 
 Flags: -O3; no fast-math (the quantizers need IEEE division and exact rounding);
 -ffp-contract=off so no multiply-add is fused behind the kernels' back (the kernels
@@ -24,6 +26,7 @@ HERE = Path(__file__).resolve().parent
 REPO = HERE.parent
 CSRC = HERE / "csrc"
 OUT = HERE / "comfy_kitchen" / "backends" / "hip" / "libckh.so"
+BENCHLIB = HERE / "benchlib"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -60,22 +63,28 @@ def _compile(src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = True) -> Path:
-    objdir = HERE / "_build"
-    objdir.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+def _link(sources: list[Path], out: Path, objdir: Path, verbose: bool) -> Path:
+    objdir.mkdir(parents=True, exist_ok=True)
     objs = [objdir / (s.stem + ".o") for s in sources]
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 8)
     with cf.ThreadPoolExecutor(max_workers=max(workers, 1)) as ex:
         list(ex.map(_compile, sources, objs))
-    tmp = OUT.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT.relative_to(REPO)} from {len(sources)} sources")
+        print(f"built {out.relative_to(REPO)} from {len(sources)} sources")
+    return out
+
+
+def build(verbose: bool = True) -> Path:
+    _link(sorted(CSRC.glob("*.hip")), OUT, HERE / "_build", verbose)
+    bench = sorted(BENCHLIB.glob("*.hip"))
+    if bench:
+        _link(bench, BENCHLIB / "libckh_bench.so", HERE / "_build" / "benchlib", verbose)
     return OUT
 
 

@@ -25,6 +25,7 @@ __all__ = [
     "quantize_per_tensor_fp8",
     "dequantize_per_tensor_fp8",
     "quantize_nvfp4",
+    "quantize_nvfp4_dynamic",
     "dequantize_nvfp4",
     "quantize_mxfp8",
     "dequantize_mxfp8",
@@ -81,6 +82,18 @@ def quantize_nvfp4(x: torch.Tensor, per_tensor_scale: torch.Tensor, epsilon: flo
                    pad_16x: bool = False, hi_first: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
     """NVFP4: packed E2M1 codes [M, K/2] uint8 and swizzled E4M3 block-16 scales."""
     return torch.ops.comfy_kitchen.quantize_nvfp4(x, per_tensor_scale, epsilon, pad_16x, hi_first)
+
+
+def quantize_nvfp4_dynamic(x: torch.Tensor, divisor: float = 448.0 * 6.0, pad_16x: bool = False,
+                           hi_first: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """quantize_nvfp4 with the per-tensor scale amax(|x|) / divisor (in x's dtype) formed on
+    the device in the same call: returns (codes, block scales, 0-dim fp32 scale).
+
+    Not part of the reference's public API: it is the scale=None branch of the NVFP4
+    layout's quantize (reference tensor/nvfp4.py:64-69, the dynamic activation scale of
+    samples/nvfp4_linear.py:55-59) with the reduction fused into the quantize launch.
+    The results equal amax_scale followed by quantize_nvfp4 bit for bit."""
+    return torch.ops.comfy_kitchen.quantize_nvfp4_dynamic(x, float(divisor), pad_16x, hi_first)
 
 
 def dequantize_nvfp4(qx: torch.Tensor, per_tensor_scale: torch.Tensor, block_scales: torch.Tensor,

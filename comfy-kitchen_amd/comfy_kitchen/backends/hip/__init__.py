@@ -32,6 +32,7 @@ __all__ = [
     "dequantize_per_tensor_fp8",
     "quantize_mxfp8",
     "quantize_nvfp4",
+    "quantize_nvfp4_dynamic",
     "quantize_per_tensor_fp8",
     "scaled_mm_fp8",
     "scaled_mm_mxfp8",
@@ -59,8 +60,9 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
     "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _p, _u64]),
     "ckh_amax_scale_noalloc": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
+    "ckh_quantize_nvfp4_dynamic": (_i32, [_p, _f32, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _p, _u64]),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 # CKH_AMAX_WORKSPACE_BYTES of include/ckh.h: the workspace ckh_amax_scale takes
 AMAX_WORKSPACE_BYTES = 8192
 
@@ -223,6 +225,30 @@ def quantize_nvfp4(x: torch.Tensor, per_tensor_scale: torch.Tensor, epsilon: flo
         _call("ckh_quantize_nvfp4", x.data_ptr(), g.data_ptr(), qx.data_ptr(), sx.data_ptr(), rows, cols,
               orows, ocols, float(epsilon), DTYPE_TO_CODE[x.dtype], int(bool(hi_first)), _stream(x))
     return qx, sx.view(torch.float8_e4m3fn)
+
+
+def quantize_nvfp4_dynamic(x: torch.Tensor, divisor: float, pad_16x: bool = False,
+                           hi_first: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """quantize_nvfp4 with the scale amax(|x|) / divisor formed on the device in the same
+    pass: (codes, block scales, 0-dim fp32 scale), equal to amax_scale + quantize_nvfp4."""
+    if x.dim() != 2:
+        raise ValueError(f"quantize_nvfp4 expects a 2-D tensor, got {x.dim()}-D")
+    x = x.contiguous()
+    if x.numel() == 0:
+        raise RuntimeError("quantize_nvfp4_dynamic: empty tensor")
+    orows, ocols = x.shape
+    rows, cols = (roundup(orows, 16), roundup(ocols, 16)) if pad_16x else (orows, ocols)
+    if cols % 16:
+        raise ValueError(f"K dimension must be divisible by 16 (got {cols}); pass pad_16x=True")
+    qx = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
+    sx = torch.empty((roundup(rows, 128), roundup(cols // 16, 4)), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((), dtype=torch.float32, device=x.device)
+    work = torch.empty(AMAX_WORKSPACE_BYTES // 4, dtype=torch.int32, device=x.device)
+    with _on_device(x):
+        _call("ckh_quantize_nvfp4_dynamic", x.data_ptr(), float(divisor), scale.data_ptr(), qx.data_ptr(),
+              sx.data_ptr(), rows, cols, orows, ocols, 0.0, DTYPE_TO_CODE[x.dtype], int(bool(hi_first)),
+              work.data_ptr(), _stream(x))
+    return qx, sx.view(torch.float8_e4m3fn), scale
 
 
 def dequantize_nvfp4(qx: torch.Tensor, per_tensor_scale: torch.Tensor, block_scales: torch.Tensor,
@@ -391,6 +417,7 @@ def _build_constraints() -> dict:
                                output_type=ParamConstraint(dtypes=floats)),
         "quantize_nvfp4": fc(x=ParamConstraint(dtypes=floats, shape_rules=two_d),
                              per_tensor_scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"}))),
+        "quantize_nvfp4_dynamic": fc(x=ParamConstraint(dtypes=floats, shape_rules=two_d)),
         "dequantize_nvfp4": fc(qx=ParamConstraint(dtypes=frozenset({torch.uint8}),
                                                   shape_rules=two_d + (DivisibleBy(1, 8),)),
                                per_tensor_scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),

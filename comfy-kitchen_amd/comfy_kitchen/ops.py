@@ -69,6 +69,22 @@ def _(x, per_tensor_scale, epsilon, pad_16x, hi_first):
     return q, s
 
 
+@torch.library.custom_op("comfy_kitchen::quantize_nvfp4_dynamic", mutates_args=())
+def quantize_nvfp4_dynamic(x: torch.Tensor, divisor: float, pad_16x: bool,
+                           hi_first: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _dispatch("quantize_nvfp4_dynamic", x=x, divisor=divisor, pad_16x=pad_16x, hi_first=hi_first)
+
+
+@quantize_nvfp4_dynamic.register_fake
+def _(x, divisor, pad_16x, hi_first):
+    rows, cols = x.shape
+    if pad_16x:
+        rows, cols = roundup(rows, 16), roundup(cols, 16)
+    q = torch.empty((rows, cols // 2), dtype=torch.uint8, device=x.device)
+    s = torch.empty((roundup(rows, 128), roundup(cols // 16, 4)), dtype=torch.float8_e4m3fn, device=x.device)
+    return q, s, torch.empty((), dtype=torch.float32, device=x.device)
+
+
 @torch.library.custom_op("comfy_kitchen::dequantize_nvfp4", mutates_args=())
 def dequantize_nvfp4(qx: torch.Tensor, per_tensor_scale: torch.Tensor, block_scales: torch.Tensor,
                      output_dtype_code: int, hi_first: bool) -> torch.Tensor:

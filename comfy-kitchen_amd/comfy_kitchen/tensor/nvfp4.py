@@ -47,14 +47,16 @@ class TensorCoreNVFP4Layout(QuantizedLayout):
 
         if tensor.dim() != 2:
             raise ValueError(f"NVFP4 requires 2D tensor, got {tensor.dim()}D")
+        shape = tuple(tensor.shape)
+        pad = cls.get_padded_shape(shape) != shape
         if scale is None or (isinstance(scale, str) and scale == "recalculate"):
-            # amax(|x|) / max in x's dtype, as one device-side reduction
-            scale = ck.amax_scale(tensor, (F8_E4M3_MAX * F4_E2M1_MAX))
+            # amax(|x|) / max in x's dtype, reduced on the device in the quantize call
+            qdata, block_scale, scale = ck.quantize_nvfp4_dynamic(tensor, F8_E4M3_MAX * F4_E2M1_MAX, pad_16x=pad)
+            return qdata, cls.Params(scale=scale, orig_dtype=tensor.dtype, orig_shape=shape, block_scale=block_scale)
         if not isinstance(scale, torch.Tensor):
             scale = torch.tensor(scale)
         scale = scale.to(device=tensor.device, dtype=torch.float32)
-        shape = tuple(tensor.shape)
-        qdata, block_scale = ck.quantize_nvfp4(tensor, scale, pad_16x=cls.get_padded_shape(shape) != shape)
+        qdata, block_scale = ck.quantize_nvfp4(tensor, scale, pad_16x=pad)
         return qdata, cls.Params(scale=scale, orig_dtype=tensor.dtype, orig_shape=shape, block_scale=block_scale)
 
     @classmethod

@@ -111,17 +111,43 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const uint32_t* __re
     uint32_t m = 0;
     for (int i = threadIdx.x; i < nblocks; i += kThreads) m = max(m, partial[i]);
     const uint32_t b = block_max(m);
-    if (threadIdx.x == 0) {
-        const float q = as_f(b) * inv_divisor;
-        float r;
-        if constexpr (IN == CKH_BF16) r = bf16_to_f(f_to_bf16(q));
-        else if constexpr (IN == CKH_F16) r = round_f16(q);
-        else r = q;
-        *out = r;
-    }
+    if (threadIdx.x == 0) *out = scale_of_amax_bits<IN>(b, inv_divisor);
 }
 
 }  // namespace am
+
+int amax_partials(const void* x, int64_t numel, int in_code, uint32_t* partial, hipStream_t st) {
+    const int es = in_code == CKH_F32 ? 4 : 2;
+    const bool vec = aligned(x, 16);
+    // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight; never
+    // more workgroups than the workspace has partial words
+    const int64_t chunks = cdiv(numel * es, 16);
+    const int blocks = static_cast<int>(
+        std::max<int64_t>(1, std::min<int64_t>(am::kMaxBlocks, cdiv(chunks, am::kThreads * am::kUnroll))));
+#define LAUNCH(I)                                                                                                \
+    do {                                                                                                         \
+        if (vec) hipLaunchKernelGGL((am::amax_kernel<I, true>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
+        else hipLaunchKernelGGL((am::amax_kernel<I, false>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
+    } while (0)
+    if (in_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+    return blocks;
+}
+
+void amax_finalize(const uint32_t* partial, int nparts, int in_code, float divisor, float* scale_out,
+                   hipStream_t st) {
+    // torch's op-math reciprocal of the scalar divisor: fp32 division on the host
+    const float inv_divisor = 1.0f / divisor;
+#define LAUNCH(I) \
+    hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(am::kThreads), 0, st, partial, nparts, inv_divisor, scale_out)
+    if (in_code == CKH_F32) LAUNCH(CKH_F32);
+    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
+    else LAUNCH(CKH_BF16);
+#undef LAUNCH
+}
+
 }  // namespace ckh
 
 using namespace ckh;
@@ -131,26 +157,8 @@ namespace {
 // Both entry points: pass 1 (per-workgroup maxima into `partial`) and pass 2 (the scale).
 int launch_amax(const void* x, int64_t numel, int in_code, float divisor, void* scale_out, uint32_t* partial,
                 hipStream_t st) {
-    // torch's op-math reciprocal of the scalar divisor: fp32 division on the host
-    const float inv_divisor = 1.0f / divisor;
-    const int es = in_code == CKH_F32 ? 4 : 2;
-    const bool vec = aligned(x, 16);
-    // up to 8 workgroups per CU, each thread with kUnroll 16-byte loads in flight; never
-    // more workgroups than the workspace has partial words
-    const int64_t chunks = cdiv(numel * es, 16);
-    const int blocks = static_cast<int>(
-        std::max<int64_t>(1, std::min<int64_t>(am::kMaxBlocks, cdiv(chunks, am::kThreads * am::kUnroll))));
-#define LAUNCH(I)                                                                                            \
-    do {                                                                                                     \
-        if (vec) hipLaunchKernelGGL((am::amax_kernel<I, true>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
-        else hipLaunchKernelGGL((am::amax_kernel<I, false>), dim3(blocks), dim3(am::kThreads), 0, st, x, numel, partial); \
-        hipLaunchKernelGGL((am::finalize_kernel<I>), dim3(1), dim3(am::kThreads), 0, st, partial, blocks, inv_divisor, \
-                           static_cast<float*>(scale_out));                                                  \
-    } while (0)
-    if (in_code == CKH_F32) LAUNCH(CKH_F32);
-    else if (in_code == CKH_F16) LAUNCH(CKH_F16);
-    else LAUNCH(CKH_BF16);
-#undef LAUNCH
+    const int blocks = amax_partials(x, numel, in_code, partial, st);
+    amax_finalize(partial, blocks, in_code, divisor, static_cast<float*>(scale_out), st);
     return CKH_OK;
 }
 

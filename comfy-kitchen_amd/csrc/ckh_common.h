@@ -299,4 +299,46 @@ __device__ __forceinline__ void grouped_tile(int L, int tiles_m, int tiles_n, in
     tn = i / gs;
 }
 
+
+// ------------------------------------------------ dynamic per-tensor scale (amax.hip)
+// Pass 1 of the layouts' default scale amax(|x|) / divisor: each workgroup of the launch
+// writes the largest |x| of its share, as ordered fp32 bits (NaN above inf), to its word
+// of `partial` (at most CKH_AMAX_WORKSPACE_BYTES / 4 words).  Returns the number of words.
+int amax_partials(const void* x, int64_t numel, int in_code, uint32_t* partial, hipStream_t st);
+// Pass 2 as its own launch: *scale_out = the scale from `nparts` partial words.
+void amax_finalize(const uint32_t* partial, int nparts, int in_code, float divisor, float* scale_out,
+                   hipStream_t st);
+
+// The scale from the partial words: round_IN(amax * inv_divisor), inv_divisor = the fp32
+// reciprocal torch multiplies by when it divides a GPU tensor by a Python scalar.
+template <int IN>
+__device__ __forceinline__ float scale_of_amax_bits(uint32_t amax_bits, float inv_divisor) {
+    const float q = as_f(amax_bits) * inv_divisor;
+    if constexpr (IN == CKH_BF16) return bf16_to_f(f_to_bf16(q));
+    else if constexpr (IN == CKH_F16) return round_f16(q);
+    else return q;
+}
+
+// Workgroup-wide reduction of the partial words to the scale, for kernels that fuse pass 2
+// into their prologue.  Every thread of the workgroup (NT threads) must call it; `red`
+// is NT / 64 words of LDS.  The barrier waits for LDS traffic only, so global loads the
+// caller issued before stay in flight (except as the partial words' own loads require).
+template <int IN, int NT>
+__device__ __forceinline__ float scale_from_partials(const uint32_t* __restrict__ partial, uint32_t nparts,
+                                                     float inv_divisor, uint32_t* red) {
+    uint32_t m = 0;
+    for (uint32_t i = threadIdx.x; i < nparts; i += NT) m = max(m, partial[i]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, 64)));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    uint32_t b = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) b = max(b, red[w]);
+    return scale_of_amax_bits<IN>(b, inv_divisor);
+}
+
 }  // namespace ckh

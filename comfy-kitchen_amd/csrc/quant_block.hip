@@ -342,12 +342,14 @@ __device__ __noinline__ uint32_t nvfp4_codes8_div_rare(float v0, float v1, float
 }
 
 // Block scale code s8 from the block amax and the global scale (IEEE divisions).
-// A NaN c keeps the sign the reference's fp32 ops give it: the amax (a |x|) NaN is
-// positive and x86 division returns its first NaN operand, so NaN amax -> 0x7F, and
-// otherwise a NaN g passes its sign; fp32 clamp(max=448) returns the NaN unchanged.
+// A NaN c keeps the sign the reference's fp32 ops give it (x86_nan): the amax (a |x|) NaN
+// is positive and division returns its first NaN operand, so NaN amax -> 0x7F; else a
+// NaN g passes its sign; else c is NaN from an invalid division (0/0 for an all-zero
+// block with g = 0, inf/inf), the default NaN 0xFFC00000 -> 0xFF.  fp32 clamp(max=448)
+// returns the NaN unchanged.
 __device__ __forceinline__ uint32_t nvfp4_scale_code_of(float c, float amax, float g) {
     c = c > 448.0f ? 448.0f : c;  // NaN passes through, as torch.clamp
-    if (is_nan(c)) return is_nan(amax) || !is_nan(g) ? 0x7fu : (0x7fu | ((as_u(g) >> 24) & 0x80u));
+    if (is_nan(c)) return 0x7fu | (is_nan(amax) ? 0u : is_nan(g) ? ((as_u(g) >> 24) & 0x80u) : 0x80u);
     // 0 <= c <= 448 here (c < 0 only for g < 0, and clamp keeps it): the hardware
     // E4M3 convert is exact on [-448, 448]
     return hw_e4m3x4(c, 0.0f, 0.0f, 0.0f) & 0xffu;
@@ -440,14 +442,21 @@ constexpr int kNvUnits = 2;  // units per thread: 2 passes cover a workgroup's 3
 // G = unit columns per item (4 or 16); the workgroup has 64*G threads.  A wave's 16
 // units in one pass are 16/G rows x G consecutive units, so with G = 16 each load
 // instruction reads 2 KB of one row.
-template <int IN, bool HI_FIRST, int G>
+// DYN: the global scale is not an input but the layouts' default, amax(|x|) / divisor,
+// formed by every workgroup from the `nparts` partial maxima that amax_partials wrote for
+// this x (scale_from_partials); workgroup 0 stores it to *scale_out.  The x loads are
+// issued first, so their latency overlaps that reduction.
+template <int IN, bool HI_FIRST, int G, bool DYN>
 __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint16_t* __restrict__ x,
                                                                      const float* __restrict__ gptr,
                                                                      uint8_t* __restrict__ qx,
                                                                      uint32_t* __restrict__ sc, uint32_t rows,
                                                                      uint32_t cols, uint32_t n_cb, uint32_t n_items,
                                                                      uint32_t n_cg, uint32_t cg_magic,
-                                                                     uint32_t cg_shift) {
+                                                                     uint32_t cg_shift,
+                                                                     const uint32_t* __restrict__ partial,
+                                                                     uint32_t nparts, float inv_divisor,
+                                                                     float* __restrict__ scale_out) {
     // item: 128 rows x G unit columns.  This workgroup: rows 8q..8q+7 of each of the
     // tile's four 32-row groups (32 rows) x G units.  Its scale words of one unit column
     // are then 32 consecutive words (one 128-byte line): staged in LDS and stored as
@@ -457,12 +466,6 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     if (!it.valid) return;
     __shared__ uint32_t sw[G * 32];
     const uint32_t l = threadIdx.x & 3;
-    const float g = gptr[0];
-    const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
-    // RN(1/g) by rcp + one Newton step: equal to the IEEE division for every g in
-    // [2^-70, 2^71), and yg is only used when g_ok
-    const float yg0 = __builtin_amdgcn_rcpf(g);
-    const float yg = __builtin_fmaf(__builtin_fmaf(-g, yg0, 1.0f), yg0, yg0);
     constexpr float y6 = 1.0f / 6.0f;
     uint4 w[kNvUnits][2];
     uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
@@ -479,6 +482,19 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
             w[u][1] = ld_stream16(x + off[u] + 8);
         }
     }
+    float g;
+    if constexpr (DYN) {
+        __shared__ uint32_t red[G];
+        g = scale_from_partials<IN, 64 * G>(partial, nparts, inv_divisor, red);
+        if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = g;
+    } else {
+        g = gptr[0];
+    }
+    const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
+    // RN(1/g) by rcp + one Newton step: equal to the IEEE division for every g in
+    // [2^-70, 2^71), and yg is only used when g_ok
+    const float yg0 = __builtin_amdgcn_rcpf(g);
+    const float yg = __builtin_fmaf(__builtin_fmaf(-g, yg0, 1.0f), yg0, yg0);
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
@@ -849,17 +865,69 @@ extern "C" int ckh_quantize_mxfp8(const void* x, void* qx, void* scales, int64_t
     return check_launch("quantize_mxfp8");
 }
 
+namespace {
+
+// The 16-bit fast path applies: no padding, whole 64-column units, aligned pointers.
+bool nvfp4_fast_applies(const void* x, const void* qx, const void* scales, int64_t rows, int64_t cols,
+                        int64_t orig_rows, int64_t orig_cols, int in_code) {
+    return (in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 64 == 0 &&
+           aligned(x, 16) && aligned(qx, 8) && aligned(scales, 16) && rup(rows, 128) * cols < (int64_t(1) << 31);
+}
+
+// items: 128-row tiles x groups of G unit columns, 4 workgroups per item; G = 16 (2 KB row
+// runs) unless a row has fewer than 16 units.  DYN: see quantize_nvfp4_fast_kernel.
+template <bool DYN>
+void launch_nvfp4_fast(const void* x, const float* g, uint8_t* q, uint32_t* s, int64_t rows, int64_t cols,
+                       int in_code, bool hf, const uint32_t* partial, uint32_t nparts, float inv_divisor,
+                       float* scale_out, hipStream_t st) {
+    const int64_t n_cb = cdiv(cols / 16, 4);
+    const int G = n_cb >= 16 ? 16 : 4;
+    const int64_t n_cg = cdiv(n_cb, G), n_items = cdiv(rows, 128) * n_cg;
+    uint32_t magic, shift;
+    magic_div(n_cg, magic, shift);
+    dim3 fgrid(static_cast<unsigned>(cdiv(n_items, 8) * 32));
+    const uint16_t* xx = static_cast<const uint16_t*>(x);
+    const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
+               n32 = static_cast<uint32_t>(n_cb), i32 = static_cast<uint32_t>(n_items),
+               g32 = static_cast<uint32_t>(n_cg);
+#define LAUNCH_FAST(I, H, GG)                                                                                    \
+    hipLaunchKernelGGL((quantize_nvfp4_fast_kernel<I, H, GG, DYN>), fgrid, dim3(64 * GG), 0, st, xx, g, q, s, r32, \
+                       c32, n32, i32, g32, magic, shift, partial, nparts, inv_divisor, scale_out)
+#define BY_G(I, H)                          \
+    do {                                    \
+        if (G == 16) LAUNCH_FAST(I, H, 16); \
+        else LAUNCH_FAST(I, H, 4);          \
+    } while (0)
+    if (in_code == CKH_BF16) {
+        if (hf) BY_G(CKH_BF16, true);
+        else BY_G(CKH_BF16, false);
+    } else {
+        if (hf) BY_G(CKH_F16, true);
+        else BY_G(CKH_F16, false);
+    }
+#undef BY_G
+#undef LAUNCH_FAST
+}
+
+int check_nvfp4_args(const void* qx, const void* scales, int64_t rows, int64_t cols, int64_t orig_rows,
+                     int64_t orig_cols, int in_code, const char* what) {
+    CKH_REQUIRE(rows >= orig_rows && cols >= orig_cols && orig_rows >= 0 && orig_cols >= 0,
+                "%s: padded shape smaller than input", what);
+    CKH_REQUIRE(cols % 16 == 0, "%s: cols (%lld) must be a multiple of 16", what, (long long)cols);
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "%s: unsupported input dtype code %d", what, in_code);
+    CKH_REQUIRE(aligned(qx, 4) && aligned(scales, 4), "%s: output pointers misaligned", what);
+    return CKH_OK;
+}
+
+}  // namespace
+
 extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void* qx, void* scales, int64_t rows,
                                   int64_t cols, int64_t orig_rows, int64_t orig_cols, float epsilon, int in_code,
                                   int hi_first, uintptr_t stream) {
     (void)epsilon;  // accepted for ABI compatibility; the reference ignores it too
     CKH_REQUIRE(x && global_scale && qx && scales, "quantize_nvfp4: null pointer");
-    CKH_REQUIRE(rows >= orig_rows && cols >= orig_cols && orig_rows >= 0 && orig_cols >= 0,
-                "quantize_nvfp4: padded shape smaller than input");
-    CKH_REQUIRE(cols % 16 == 0, "quantize_nvfp4: cols (%lld) must be a multiple of 16", (long long)cols);
-    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
-                "quantize_nvfp4: unsupported input dtype code %d", in_code);
-    CKH_REQUIRE(aligned(qx, 4) && aligned(scales, 4), "quantize_nvfp4: output pointers misaligned");
+    if (int rc = check_nvfp4_args(qx, scales, rows, cols, orig_rows, orig_cols, in_code, "quantize_nvfp4")) return rc;
     if (rows == 0 || cols == 0) return CKH_OK;
     const int64_t n_cb = cdiv(cols / 16, 4);
     const int64_t n_units = rup(rows, 128) * n_cb;
@@ -869,36 +937,8 @@ extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void*
     uint8_t* q = static_cast<uint8_t*>(qx);
     uint32_t* s = static_cast<uint32_t*>(scales);
     const bool hf = hi_first != 0;
-    if ((in_code == CKH_BF16 || in_code == CKH_F16) && rows == orig_rows && cols == orig_cols && cols % 64 == 0 &&
-        aligned(x, 16) && aligned(qx, 8) && aligned(scales, 16) && rup(rows, 128) * cols < (int64_t(1) << 31)) {
-        // items: 128-row tiles x groups of G unit columns, 4 workgroups per item; G = 16
-        // (2 KB row runs) unless a row has fewer than 16 units
-        const int G = n_cb >= 16 ? 16 : 4;
-        const int64_t n_cg = cdiv(n_cb, G), n_items = cdiv(rows, 128) * n_cg;
-        uint32_t magic, shift;
-        magic_div(n_cg, magic, shift);
-        dim3 fgrid(static_cast<unsigned>(cdiv(n_items, 8) * 32));
-        const uint16_t* xx = static_cast<const uint16_t*>(x);
-        const auto r32 = static_cast<uint32_t>(rows), c32 = static_cast<uint32_t>(cols),
-                   n32 = static_cast<uint32_t>(n_cb), i32 = static_cast<uint32_t>(n_items),
-                   g32 = static_cast<uint32_t>(n_cg);
-#define LAUNCH_FAST(I, H, GG)                                                                                     \
-    hipLaunchKernelGGL((quantize_nvfp4_fast_kernel<I, H, GG>), fgrid, dim3(64 * GG), 0, st, xx, g, q, s, r32, c32, \
-                       n32, i32, g32, magic, shift)
-#define BY_G(I, H)                     \
-    do {                               \
-        if (G == 16) LAUNCH_FAST(I, H, 16); \
-        else LAUNCH_FAST(I, H, 4);          \
-    } while (0)
-        if (in_code == CKH_BF16) {
-            if (hf) BY_G(CKH_BF16, true);
-            else BY_G(CKH_BF16, false);
-        } else {
-            if (hf) BY_G(CKH_F16, true);
-            else BY_G(CKH_F16, false);
-        }
-#undef BY_G
-#undef LAUNCH_FAST
+    if (nvfp4_fast_applies(x, qx, scales, rows, cols, orig_rows, orig_cols, in_code)) {
+        launch_nvfp4_fast<false>(x, g, q, s, rows, cols, in_code, hf, nullptr, 0u, 0.0f, nullptr, st);
         return check_launch("quantize_nvfp4");
     }
     dim3 grid(static_cast<unsigned>(cdiv(n_units * 8, kThreads)));
@@ -916,6 +956,32 @@ extern "C" int ckh_quantize_nvfp4(const void* x, const void* global_scale, void*
 #undef BY_ORDER
 #undef LAUNCH
     return check_launch("quantize_nvfp4");
+}
+
+extern "C" int ckh_quantize_nvfp4_dynamic(const void* x, float divisor, void* scale_out, void* qx, void* scales,
+                                          int64_t rows, int64_t cols, int64_t orig_rows, int64_t orig_cols,
+                                          float epsilon, int in_code, int hi_first, void* workspace,
+                                          uintptr_t stream) {
+    CKH_REQUIRE(x && scale_out && qx && scales && workspace, "quantize_nvfp4_dynamic: null pointer");
+    if (int rc = check_nvfp4_args(qx, scales, rows, cols, orig_rows, orig_cols, in_code, "quantize_nvfp4_dynamic"))
+        return rc;
+    CKH_REQUIRE(orig_rows > 0 && orig_cols > 0,
+                "quantize_nvfp4_dynamic: empty tensor (torch.amax of an empty tensor is an error too)");
+    CKH_REQUIRE(aligned(scale_out, 4) && aligned(workspace, 4), "quantize_nvfp4_dynamic: scale or workspace misaligned");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint32_t* partial = static_cast<uint32_t*>(workspace);
+    const int nparts = amax_partials(x, orig_rows * orig_cols, in_code, partial, st);
+    if (nvfp4_fast_applies(x, qx, scales, rows, cols, orig_rows, orig_cols, in_code)) {
+        launch_nvfp4_fast<true>(x, nullptr, static_cast<uint8_t*>(qx), static_cast<uint32_t*>(scales), rows, cols,
+                                in_code, hi_first != 0, partial, static_cast<uint32_t>(nparts), 1.0f / divisor,
+                                static_cast<float*>(scale_out), st);
+        return check_launch("quantize_nvfp4_dynamic");
+    }
+    // other shapes: the scale as its own launch, then the general quantize reading it
+    amax_finalize(partial, nparts, in_code, divisor, static_cast<float*>(scale_out), st);
+    if (int rc = check_launch("quantize_nvfp4_dynamic")) return rc;
+    return ckh_quantize_nvfp4(x, scale_out, qx, scales, rows, cols, orig_rows, orig_cols, epsilon, in_code, hi_first,
+                              stream);
 }
 
 extern "C" int ckh_dequantize_mxfp8(const void* qx, const void* scales, void* out, int64_t rows, int64_t cols,

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 4
+#define CKH_ABI_VERSION 5
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -198,6 +198,26 @@ int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, voi
  */
 int ckh_amax_scale_noalloc(const void* x, int64_t numel, int in_code, float divisor,
                            void* scale_out, uintptr_t stream);
+
+/*
+ * NVFP4 quantize with the layouts' dynamic global scale: ckh_amax_scale (divisor 2688 for
+ * TensorCoreNVFP4Layout) followed by ckh_quantize_nvfp4 with that scale, in two launches
+ * instead of three.  Launch 1 writes the per-workgroup partial maxima of |x| to
+ * `workspace` (CKH_AMAX_WORKSPACE_BYTES, 4-byte aligned; its loads are cached, so the
+ * quantize that follows finds x in the 256 MB infinity cache when it fits there); launch 2
+ * quantizes, every workgroup forming the scale from those words itself, and stores the
+ * scale to *scale_out (one f32 on device).  Codes, block scales and *scale_out equal those
+ * of the two separate calls bit for bit.  Shapes and arguments as ckh_quantize_nvfp4,
+ * plus x non-empty; shapes outside the 16-bit fast path (padding, f32 input, cols % 64,
+ * alignment) run the separate scale launch and the general quantize.  Calls running at
+ * the same time need workspaces of their own.  Replaces the scale=None branch of
+ * TensorCoreNVFP4Layout.quantize (tensor/nvfp4.py:64-69: torch.amax(x.abs()) / 2688, then
+ * ck.quantize_nvfp4), the dynamic input quantization of samples/nvfp4_linear.py:55-59.
+ */
+int ckh_quantize_nvfp4_dynamic(const void* x, float divisor, void* scale_out, void* qx, void* scales,
+                               int64_t rows, int64_t cols, int64_t orig_rows, int64_t orig_cols,
+                               float epsilon, int in_code, int hi_first, void* workspace,
+                               uintptr_t stream);
 
 #ifdef __cplusplus
 }

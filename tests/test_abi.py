@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 4
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 5
 
 
 def test_amax_workspace_size_matches_header():
@@ -73,3 +73,15 @@ def test_invalid_arguments_return_error(lib):
 def test_zero_sized_calls_are_noops(lib):
     assert lib.ckh_quantize_fp8(None, None, None, 0, 2, 5, 0) == 0
     assert lib.ckh_dequantize_fp8(None, None, None, 0, 5, 2, 0) == 0
+
+
+def test_quantize_nvfp4_dynamic_rejects_bad_arguments(lib):
+    buf = ctypes.create_string_buffer(256)
+    p = ctypes.addressof(buf)
+    f = lib.ckh_quantize_nvfp4_dynamic
+    assert f(p, 2688.0, p, p, p, 16, 64, 16, 64, 0.0, 2, 1, None, 0) == 1  # no workspace
+    assert b"null pointer" in lib.ckh_last_error()
+    assert f(p, 2688.0, p, p, p, 0, 64, 0, 64, 0.0, 2, 1, p, 0) == 1
+    assert b"empty tensor" in lib.ckh_last_error()
+    assert f(p, 2688.0, p, p, p, 16, 40, 16, 40, 0.0, 2, 1, p, 0) == 1
+    assert b"multiple of 16" in lib.ckh_last_error()

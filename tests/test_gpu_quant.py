@@ -282,11 +282,15 @@ def test_quantize_nvfp4_special_blocks(dtype, hi_first, hip, seed):
     _check_nv(x, g, pad=False, hi_first=hi_first)
 
 
-@pytest.mark.parametrize("g", [1.0, 1e-30, 1e-40, 0.0, -0.01, 1e20, 3.0e-3])
+@pytest.mark.parametrize("g", [1.0, 1e-30, 1e-40, 0.0, -0.0, -0.01, 1e20, 3.0e-3, float("inf"), float("nan")])
 def test_quantize_nvfp4_global_scale_edges(g, hip, seed):
     # global scales outside the fast path's range (zero, subnormal, negative, huge) take
-    # the IEEE-division path inside the same kernel
+    # the IEEE-division path inside the same kernel.  With g = 0 the all-zero block's
+    # 0/0 and with g = inf the infinite block's inf/inf are invalid divisions: x86 gives
+    # the negative default NaN, so scale byte 0xFF and negative-NaN codes.
     x = torch.randn(130, 128) * torch.exp(torch.randn(130, 1) * 3)
+    x[2, :16] = 0.0
+    x[3, 16] = float("inf")
     # with g = 1 this block has T = 1 exactly, so its values sit on the E2M1 rounding
     # boundaries (ties go to the even code)
     x[1, :16] = torch.tensor([6.0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5.0, 0.5])
@@ -412,3 +416,62 @@ def test_layout_dynamic_scale_uses_the_reference_default(layout, hip, seed):
         q, s = ref.quantize_nvfp4(x, want.reshape(1))
         assert torch.equal(qt._qdata.cpu(), q)
         assert torch.equal(bits(qt._params.block_scale), bits(s))
+
+
+# ----------------------------------------------------- fused dynamic NVFP4 quantize
+def _check_nv_dynamic(x, pad=False, hi_first=True, oracle=True):
+    """quantize_nvfp4_dynamic == amax_scale + quantize_nvfp4 on the device, and (oracle=True)
+    == the oracle's default_scale + quantize_nvfp4, bit for bit (codes, block scales, scale)."""
+    xd = x.cuda()
+    q, s, g = ck.quantize_nvfp4_dynamic(xd, 2688.0, pad_16x=pad, hi_first=hi_first)
+    assert g.shape == () and g.dtype == torch.float32
+    g2 = ck.amax_scale(xd, 2688.0)
+    q2, s2 = ck.quantize_nvfp4(xd, g2, pad_16x=pad, hi_first=hi_first)
+    assert torch.equal(bits(g), bits(g2)), (g.item(), g2.item())
+    assert torch.equal(q, q2), f"{int((q != q2).sum())} code bytes differ from the two-call path"
+    assert torch.equal(bits(s), bits(s2)), "block scales differ from the two-call path"
+    if oracle:
+        want_g = ref.default_scale(x, 2688.0)
+        assert torch.equal(bits(g), bits(want_g)), (g.item(), want_g.item())
+        want_q, want_s = ref.quantize_nvfp4(x, want_g.reshape(1), pad_16x=pad, hi_first=hi_first)
+        assert torch.equal(q.cpu(), want_q) and torch.equal(bits(s), bits(want_s))
+
+
+@pytest.mark.parametrize("hi_first", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,k,pad", [(1024, 2048, False), (512, 1024, False), (130, 192, False), (257, 320, False),
+                                     (1, 64, False), (16, 1600, False), (33, 65, True), (129, 128, True)])
+def test_quantize_nvfp4_dynamic(dtype, m, k, pad, hi_first, hip, seed):
+    x = (torch.randn(m, k) * torch.exp(torch.randn(m, 1) * 2)).to(dtype)
+    x[0, :16] = 0
+    _check_nv_dynamic(x, pad=pad, hi_first=hi_first)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ["zeros", "nan", "inf", "tiny", "huge"])
+def test_quantize_nvfp4_dynamic_special(dtype, case, hip, seed):
+    x = torch.randn(256, 512) * torch.exp(torch.randn(256, 1))
+    if case == "zeros":
+        x.zero_()
+    elif case == "nan":
+        x[100, 37] = float("nan")
+    elif case == "inf":
+        x[7, 300] = float("-inf")
+    elif case == "tiny":
+        x *= 1e-6
+    else:
+        x *= 1e4 if dtype == torch.float16 else 1e30
+    x = x.to(dtype)
+    _check_nv_dynamic(x, oracle=case != "nan")  # NaN payloads: compared with the device path only
+
+
+def test_quantize_nvfp4_dynamic_config5_activation(hip):
+    import bench
+
+    a, _, _, _ = bench.make_c5()
+    ad = a.cuda()
+    q, s, g = ck.quantize_nvfp4_dynamic(ad, 2688.0)
+    assert torch.equal(bits(g), bits(ref.default_scale(a, 2688.0)))
+    q2, s2 = ck.quantize_nvfp4(ad, g.reshape(1))
+    assert torch.equal(q, q2) and torch.equal(bits(s), bits(s2))
+    _check_nv(a, g.cpu().reshape(1), pad=False)
