@@ -241,6 +241,47 @@ __device__ __forceinline__ void st_stream8(void* p, uint2 v) {
 
 // Load 8 consecutive elements of dtype code C as floats from an address aligned to
 // 8 * sizeof(element), as a streaming read.
+// v from another lane of the row of 16 selected by the DPP control CTRL (e.g. 0xB1 =
+// quad_perm [1,0,3,2], the neighbouring lane).  Every lane the control reads must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
+// load8 in two steps, so a kernel can issue its data loads before anything that must
+// wait (e.g. a device scalar it reads): the raw 16-byte chunks of 8 elements (two for f32),
+// then their values.
+template <int C>
+struct Raw8 {
+    uint4 a, b;
+};
+template <int C>
+__device__ __forceinline__ Raw8<C> load8_raw(const void* p) {
+    Raw8<C> r;
+    r.a = ld_stream16(p);
+    r.b = C == CKH_F32 ? ld_stream16(static_cast<const char*>(p) + 16) : make_uint4(0u, 0u, 0u, 0u);
+    return r;
+}
+template <int C>
+__device__ __forceinline__ void unpack8(const Raw8<C>& r, float (&v)[8]) {
+    if constexpr (C == CKH_F32) {
+        v[0] = as_f(r.a.x); v[1] = as_f(r.a.y); v[2] = as_f(r.a.z); v[3] = as_f(r.a.w);
+        v[4] = as_f(r.b.x); v[5] = as_f(r.b.y); v[6] = as_f(r.b.z); v[7] = as_f(r.b.w);
+    } else {
+        const uint32_t d[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (C == CKH_BF16) {
+                v[2 * i] = bf16_to_f(d[i] & 0xffffu);
+                v[2 * i + 1] = bf16_to_f(d[i] >> 16);
+            } else {
+                v[2 * i] = f16_to_f(d[i] & 0xffffu);
+                v[2 * i + 1] = f16_to_f(d[i] >> 16);
+            }
+        }
+    }
+}
+
 template <int C>
 __device__ __forceinline__ void load8(const void* p, float (&v)[8]) {
     if constexpr (C == CKH_F32) {

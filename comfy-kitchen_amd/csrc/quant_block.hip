@@ -151,10 +151,6 @@ __device__ __forceinline__ uint32_t amax16x8(uint4 w) {
     return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y));
 }
 
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
-}
 
 // 16-bit amax bits -> fp32 bits of the same value
 template <int IN>

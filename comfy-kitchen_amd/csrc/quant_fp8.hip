@@ -35,16 +35,20 @@ template <int IN, int OUT, bool VEC>
 __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __restrict__ x,
                                                                 const float* __restrict__ scale,
                                                                 uint8_t* __restrict__ out, int64_t n) {
-    const float r = round_to<IN>(1.0f / scale[0]);
     // a wave's 1024 elements: lane l takes the 8-element pieces l and 64 + l, so every load
     // and store instruction covers one contiguous run
     const int64_t wbase = (static_cast<int64_t>(blockIdx.x) * kThreads + (threadIdx.x & ~63u)) * kPerThread;
     const int64_t ia = wbase + 8 * (threadIdx.x & 63u), ib = ia + 512;
     constexpr int ES = ElemSize<IN>::value;
     if (VEC && ib + 8 <= n) {
+        // the data loads go out before the scale is read and inverted, so the two
+        // latencies overlap instead of adding up
+        const Raw8<IN> ra = load8_raw<IN>(static_cast<const char*>(x) + ia * ES);
+        const Raw8<IN> rb = load8_raw<IN>(static_cast<const char*>(x) + ib * ES);
+        const float r = round_to<IN>(1.0f / scale[0]);
         float v[16];
-        load8<IN>(static_cast<const char*>(x) + ia * ES, *reinterpret_cast<float(*)[8]>(&v[0]));
-        load8<IN>(static_cast<const char*>(x) + ib * ES, *reinterpret_cast<float(*)[8]>(&v[8]));
+        unpack8<IN>(ra, *reinterpret_cast<float(*)[8]>(&v[0]));
+        unpack8<IN>(rb, *reinterpret_cast<float(*)[8]>(&v[8]));
         // hardware path: product rounded to x's dtype, clamped, converted in pairs
         float t[16];
         bool any_nan = false;
@@ -74,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
         st_stream8(out + ia, make_uint2(w[0], w[1]));
         st_stream8(out + ib, make_uint2(w[2], w[3]));
     } else {
+        const float r = round_to<IN>(1.0f / scale[0]);
         for (int64_t i = ia; i < n && i < ia + 8; ++i)
             out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
         for (int64_t i = ib; i < n && i < ib + 8; ++i)
@@ -132,15 +137,16 @@ template <int IN, int OUT, bool VEC>
 __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t* __restrict__ x,
                                                                   const float* __restrict__ scale,
                                                                   void* __restrict__ out, int64_t n) {
-    const float s = round_to<OUT>(scale[0]);
     // a wave's 1024 codes: lane l takes the 8-code pieces l and 64 + l, so every load and
     // store instruction covers one contiguous run
     const int64_t wbase = (static_cast<int64_t>(blockIdx.x) * kThreads + (threadIdx.x & ~63u)) * kPerThread;
     const int64_t ia = wbase + 8 * (threadIdx.x & 63u), ib = ia + 512;
     if (VEC && ib + 8 <= n) {
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        // the code loads go out before the scale is read and rounded
         const u32x2 ca = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ia));
         const u32x2 cb = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ib));
+        const float s = round_to<OUT>(scale[0]);
         uint32_t cw[4] = {ca.x, ca.y, cb.x, cb.y};
         // a NaN code (0x7f / 0xff in E4M3) takes the software path, which fixes its bytes
         bool nan_code = false;
@@ -166,6 +172,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
             store16<OUT>(out, ia, ib, v);
         }
     } else {
+        const float s = round_to<OUT>(scale[0]);
         for (int64_t i = ia; i < n && i < ia + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
         for (int64_t i = ib; i < n && i < ib + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
     }
