@@ -5,7 +5,8 @@
 Every csrc/*.hip file is compiled by hipcc for gfx950 only and linked into
 comfy_kitchen/backends/hip/libckh.so, which the "hip" backend loads with ctypes.
 benchlib/*.hip (kernels bench.py times for comparison, e.g. the copy floor) is linked
-into benchlib/libckh_bench.so, separate from the product library.
+into benchlib/libckh_bench.so, and tests/hw/*.hip (exhaustive hardware-identity checks)
+into tests/hw/libckh_hwcheck.so, both separate from the product library.
 
 Flags: -O3; no fast-math (the quantizers need IEEE division and exact rounding);
 -ffp-contract=off so no multiply-add is fused behind the kernels' back (the kernels
@@ -27,6 +28,7 @@ REPO = HERE.parent
 CSRC = HERE / "csrc"
 OUT = HERE / "comfy_kitchen" / "backends" / "hip" / "libckh.so"
 BENCHLIB = HERE / "benchlib"
+HWCHECK = REPO / "tests" / "hw"  # test-only: exhaustive hardware-identity sweeps
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -85,6 +87,9 @@ def build(verbose: bool = True) -> Path:
     bench = sorted(BENCHLIB.glob("*.hip"))
     if bench:
         _link(bench, BENCHLIB / "libckh_bench.so", HERE / "_build" / "benchlib", verbose)
+    hw = sorted(HWCHECK.glob("*.hip"))
+    if hw:
+        _link(hw, HWCHECK / "libckh_hwcheck.so", HERE / "_build" / "hwcheck", verbose)
     return OUT
 
 

@@ -37,12 +37,13 @@
 #include <utility>
 
 #include "ckh_common.h"
+#include "quant_math.h"
 
 namespace ckh {
 namespace nv {
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+using ckh::v8h;
+using ckh::v2h;
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -154,19 +155,6 @@ struct Dec {
     v8h b[4], a[4];
 };
 
-// 4 bytes of E2M1 codes -> 8 fp16, times the block scale pair s (exact).
-__device__ __forceinline__ v8h decode8(uint32_t w, v2h s) {
-    const v2h e0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s;
-    const v2h e1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s;
-    const v2h e2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s;
-    const v2h e3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s;
-    return v8h{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
-}
-
-// The lane half's two block scales (bytes 2h and 2h+1 of the word) as fp16; sh = 16 h.
-__device__ __forceinline__ v2h scale_pair(uint32_t word, int sh) {
-    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word >> sh, 1.0f, false);
-}
 
 template <int OUT>
 __device__ __forceinline__ uint32_t pack2(float x, float y) {

@@ -12,6 +12,7 @@
 //   MXFP8: 32-element blocks, 4 lanes per block, 16 lanes per unit.
 //   NVFP4: 16-element blocks, 2 lanes per block,  8 lanes per unit.
 #include "ckh_common.h"
+#include "quant_math.h"
 
 namespace ckh {
 
@@ -46,29 +47,6 @@ __device__ __forceinline__ uint32_t absmax_bits(const float (&v)[8]) {
 }
 
 // ------------------------------------------------------------------- MXFP8
-// E8M0 exponent of a block from its amax bits (reference eager quantization.py:292-302):
-//   s = max(amax/448, 2^-127); e = clamp(ceil(log2 s) + 127, 0, 254).
-// ceil(log2 s) is taken exactly from the bit fields of s: for normal s it is the
-// unbiased exponent plus one if any mantissa bit is set; s = 2^-127 (the clamp) gives
-// e = 0 and the only other subnormals, 2^-127 < s < 2^-126, give e = 1.  Non-finite
-// amax gives e = 0, as the reference's float->int32 conversion of ceil(log2(inf/NaN))
-// does on x86.
-//
-// For amax with a biased exponent >= 10 the division folds away: amax/448 =
-// (1.f / 1.75) * 2^(E-8) with 1.f the significand, so s is a power of two only when
-// 1.f == 1.75 exactly, and e = E - 8 + (f > 0.75).  (Checked against the division form
-// on all 2^31 non-negative floats.)
-__device__ __forceinline__ uint32_t mx_exponent(uint32_t amax_bits) {
-    if (amax_bits >= (10u << 23) && amax_bits < 0x7f800000u)
-        return (amax_bits >> 23) - 8u + ((amax_bits & 0x7fffffu) > 0x600000u);
-    if (amax_bits == 0 || amax_bits >= 0x7f800000u) return 0;
-    uint32_t s = as_u(as_f(amax_bits) / 448.0f);
-    if (s <= 0x00400000u) return 0;
-    if (s < 0x00800000u) return 1;
-    uint32_t e = (s >> 23) + ((s & 0x7fffffu) != 0);
-    return e > 254u ? 254u : e;
-}
-
 // Codes for one lane's 8 values given the block's amax bits and exponent.
 __device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_bits, uint32_t e) {
     uint32_t w[2] = {0u, 0u};
@@ -139,10 +117,6 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __
 //   * the scale word is OR-combined with two DPP row_ror steps.
 // Blocks whose amax is zero, tiny (biased exponent < 10) or non-finite take the
 // general encoder.
-typedef unsigned short ckh_u16x2 __attribute__((ext_vector_type(2)));
-typedef short ckh_i16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 ckh_bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 ckh_f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t amax16x8(uint4 w) {
     auto h = [](uint32_t v) { return __builtin_bit_cast(ckh_u16x2, v & 0x7fff7fffu); };
@@ -157,20 +131,6 @@ template <int IN>
 __device__ __forceinline__ uint32_t amax16_to_f32_bits(uint32_t m) {
     if constexpr (IN == CKH_BF16) return m << 16;
     else return as_u(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(m))));
-}
-
-// Codes of the two packed pairs a, b: E4M3(x / 2^(e-127)), scale = 2^(e-127).
-template <int IN>
-__device__ __forceinline__ uint32_t scaled_e4m3x4(uint32_t a, uint32_t b, float scale) {
-    ckh_i16x2 o = {0, 0};
-    if constexpr (IN == CKH_BF16) {
-        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, a), scale, false);
-        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, b), scale, true);
-    } else {
-        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, a), scale, false);
-        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, b), scale, true);
-    }
-    return __builtin_bit_cast(uint32_t, o);
 }
 
 template <int IN>
@@ -267,20 +227,6 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uin
 // Per 16-element block (reference eager quantization.py:137-158):
 //   s8 = E4M3(min(amax/6/g, 448)); T = g*s8; codes = E2M1(clamp(x/T, +-6)), T==0 -> +0.
 // Divisions are IEEE fp32 divisions, as in the reference's eager path.
-
-// Pack 8 non-NaN values into E2M1 nibbles with the hardware convert: RNE, identical to
-// f_to_e2m1 of the value clamped to [-6, 6] (the convert saturates), and the first
-// operand lands in the low nibble.
-template <bool HI_FIRST>
-__device__ __forceinline__ uint32_t pack_e2m1x8(const float* q) {
-    const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of each pair that goes to the low nibble
-    uint32_t w = 0;
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[0 + f], q[0 + o], 1.0f, 0);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[2 + f], q[2 + o], 1.0f, 1);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[4 + f], q[4 + o], 1.0f, 2);
-    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[6 + f], q[6 + o], 1.0f, 3);
-    return w;
-}
 
 // NaN blocks: E2M1 has no NaN code, so the reference's codes for NaN data depend on the
 // NaN's bits as its CPU arithmetic (x86 SSE) propagates them: a NaN operand is returned
@@ -417,19 +363,11 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 template <bool HI_FIRST, bool RCP = false>
 __device__ __forceinline__ uint2 nvfp4_codes16_exact(const float (&v)[16], float T) {
     float y;
-    if constexpr (RCP) {
-        const float y0 = __builtin_amdgcn_rcpf(T);
-        y = __builtin_fmaf(__builtin_fmaf(-T, y0, 1.0f), y0, y0);
-    } else {
-        y = 1.0f / T;
-    }
+    if constexpr (RCP) y = rcp_newton(T);
+    else y = 1.0f / T;
     float q[16];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        const float q0 = v[t] * y;
-        const float e = __builtin_fmaf(T, q0, -v[t]);
-        q[t] = __builtin_fmaf(-e, y, q0);
-    }
+    for (int t = 0; t < 16; ++t) q[t] = markstein_quotient(v[t], T, y);
     return make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
 }
 
@@ -462,7 +400,6 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     if (!it.valid) return;
     __shared__ uint32_t sw[G * 32];
     const uint32_t l = threadIdx.x & 3;
-    constexpr float y6 = 1.0f / 6.0f;
     uint4 w[kNvUnits][2];
     uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
 #pragma unroll
@@ -489,16 +426,12 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     const bool g_ok = g >= 0x1p-60f && g <= 0x1p60f;  // false for NaN
     // RN(1/g) by rcp + one Newton step: equal to the IEEE division for every g in
     // [2^-70, 2^71), and yg is only used when g_ok
-    const float yg0 = __builtin_amdgcn_rcpf(g);
-    const float yg = __builtin_fmaf(__builtin_fmaf(-g, yg0, 1.0f), yg0, yg0);
+    const float yg = rcp_newton(g);
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
         // the scale by the exact steps (valid when g and amax are within [2^-60, 2^60])
-        const float c0 = amax * y6;
-        const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
-        const float d0 = c1 * yg;
-        const float cf = __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
+        const float cf = nvfp4_c_steps(amax, g, yg);
         const uint32_t s8f = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(cf, 0.0f, 0, false)) & 0xffu;
         float v[16];
         unpack16x8<IN>(w[u][0], *reinterpret_cast<float(*)[8]>(&v[0]));

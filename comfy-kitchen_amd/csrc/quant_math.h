@@ -1,0 +1,117 @@
+// Exact arithmetic steps of the block quantizers' fast paths (quant_block.hip), in a
+// header so that the exhaustive hardware checks (tests/hw/identities.hip) test these very
+// functions.  Each is exact, or equal to the reference's IEEE operation, on the domain
+// stated with it; the callers keep to those domains and take IEEE paths elsewhere.
+#pragma once
+
+#include "ckh_common.h"
+
+namespace ckh {
+
+typedef unsigned short ckh_u16x2 __attribute__((ext_vector_type(2)));
+typedef short ckh_i16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ckh_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 ckh_f16x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------- MXFP8
+// E8M0 exponent of a block from its amax bits (reference eager quantization.py:292-302):
+//   s = max(amax/448, 2^-127); e = clamp(ceil(log2 s) + 127, 0, 254).
+// ceil(log2 s) is taken exactly from the bit fields of s: for normal s it is the
+// unbiased exponent plus one if any mantissa bit is set; s = 2^-127 (the clamp) gives
+// e = 0 and the only other subnormals, 2^-127 < s < 2^-126, give e = 1.  Non-finite
+// amax gives e = 0, as the reference's float->int32 conversion of ceil(log2(inf/NaN))
+// does on x86.
+//
+// For amax with a biased exponent >= 10 the division folds away: amax/448 =
+// (1.f / 1.75) * 2^(E-8) with 1.f the significand, so s is a power of two only when
+// 1.f == 1.75 exactly, and e = E - 8 + (f > 0.75).  (Checked against the division form
+// on all 2^31 non-negative floats.)
+__device__ __forceinline__ uint32_t mx_exponent(uint32_t amax_bits) {
+    if (amax_bits >= (10u << 23) && amax_bits < 0x7f800000u)
+        return (amax_bits >> 23) - 8u + ((amax_bits & 0x7fffffu) > 0x600000u);
+    if (amax_bits == 0 || amax_bits >= 0x7f800000u) return 0;
+    uint32_t s = as_u(as_f(amax_bits) / 448.0f);
+    if (s <= 0x00400000u) return 0;
+    if (s < 0x00800000u) return 1;
+    uint32_t e = (s >> 23) + ((s & 0x7fffffu) != 0);
+    return e > 254u ? 254u : e;
+}
+
+// Codes of the two packed pairs a, b: E4M3(x / 2^(e-127)), scale = 2^(e-127).
+template <int IN>
+__device__ __forceinline__ uint32_t scaled_e4m3x4(uint32_t a, uint32_t b, float scale) {
+    ckh_i16x2 o = {0, 0};
+    if constexpr (IN == CKH_BF16) {
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, a), scale, false);
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(ckh_bf16x2, b), scale, true);
+    } else {
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, a), scale, false);
+        o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(ckh_f16x2, b), scale, true);
+    }
+    return __builtin_bit_cast(uint32_t, o);
+}
+
+// Pack 8 non-NaN values into E2M1 nibbles with the hardware convert: RNE, identical to
+// f_to_e2m1 of the value clamped to [-6, 6] (the convert saturates), and the first
+// operand lands in the low nibble.
+template <bool HI_FIRST>
+__device__ __forceinline__ uint32_t pack_e2m1x8(const float* q) {
+    const int f = HI_FIRST ? 1 : 0, o = 1 - f;  // element of each pair that goes to the low nibble
+    uint32_t w = 0;
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[0 + f], q[0 + o], 1.0f, 0);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[2 + f], q[2 + o], 1.0f, 1);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[4 + f], q[4 + o], 1.0f, 2);
+    w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, q[6 + f], q[6 + o], 1.0f, 3);
+    return w;
+}
+
+// RN(1/T) from v_rcp_f32 and one FMA Newton step: equal to the IEEE 1.0f / T for every
+// float T in [2^-70, 2^71).
+__device__ __forceinline__ float rcp_newton(float T) {
+    const float y0 = __builtin_amdgcn_rcpf(T);
+    return __builtin_fmaf(__builtin_fmaf(-T, y0, 1.0f), y0, y0);
+}
+
+// v / T by one Markstein correction of v * y, y = RN(1/T): q0 = v*y, e = fma(T, q0, -v),
+// q = fma(-e, y, q0).  Its E2M1 code equals that of the IEEE quotient for every bf16 and
+// f16 v (both signs, and +-0) and every T whose products stay normal (the negated
+// residual keeps the sign of a zero v).
+__device__ __forceinline__ float markstein_quotient(float v, float T, float y) {
+    const float q0 = v * y;
+    const float e = __builtin_fmaf(T, q0, -v);
+    return __builtin_fmaf(-e, y, q0);
+}
+
+// (amax / 6) / g by two Markstein steps with the constant RN(1/6) and yg = RN(1/g):
+// bit-identical to the two IEEE divisions for every bf16 / f16 amax significand and every
+// g significand while g and amax lie within [2^-60, 2^60].
+__device__ __forceinline__ float nvfp4_c_steps(float amax, float g, float yg) {
+    constexpr float y6 = 1.0f / 6.0f;
+    const float c0 = amax * y6;
+    const float c1 = __builtin_fmaf(-__builtin_fmaf(6.0f, c0, -amax), y6, c0);
+    const float d0 = c1 * yg;
+    return __builtin_fmaf(-__builtin_fmaf(g, d0, -c1), yg, d0);
+}
+
+// ----------------------------------------------------- NVFP4 GEMM operand decode
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// 4 bytes of E2M1 codes -> 8 fp16 (low nibble first), times the block scale pair s.
+// Exact: E2M1 x E4M3 products have at most 6 significant bits and lie in [2^-10, 2688]
+// (or are zero), all fp16 normals.
+__device__ __forceinline__ v8h decode8(uint32_t w, v2h s) {
+    const v2h e0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s;
+    const v2h e1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s;
+    const v2h e2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s;
+    const v2h e3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s;
+    return v8h{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
+}
+
+// Two E4M3 block scales (bytes sh/8 and sh/8 + 1 of the word) as fp16; exact for every
+// finite code.
+__device__ __forceinline__ v2h scale_pair(uint32_t word, int sh) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word >> sh, 1.0f, false);
+}
+
+}  // namespace ckh

@@ -6,6 +6,11 @@ and its NVFP4 sample loader rebuilds the layer from "weight", "weight_scale",
 "weight_scale_2" and an optional "input_scale" (`samples/nvfp4_linear.py:39-68`).  These
 tests write the layouts' state dicts to a safetensors file, load it back with the safe
 loader, rebuild the tensors the way that loader does, and check every byte survives.
+
+tests/golden/checkpoints.safetensors (made by tests/golden/make_checkpoints.py with the CPU
+oracle) holds one layer per layout in that key convention plus the oracle's outputs; the
+GPU tests load it as the reference's loaders do and compare F.linear with the oracle, and
+re-quantize its source weight on the GPU and compare the bytes.
 """
 import pytest
 import torch
@@ -108,3 +113,93 @@ def test_reloaded_weight_gives_the_same_linear(make, tmp_path, hip):
     want = torch.nn.functional.linear(x, original)
     got = torch.nn.functional.linear(x, reloaded)
     assert torch.equal(got, want)
+
+
+# ------------------------------------------------- committed fixture (oracle-made)
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden" / "checkpoints.safetensors"
+LAYOUTS = {"fp8": "TensorCoreFP8Layout", "mxfp8": "TensorCoreMXFP8Layout", "nvfp4": "TensorCoreNVFP4Layout"}
+
+
+def _golden():
+    return load_file(str(GOLDEN))
+
+
+def test_golden_checkpoint_is_what_the_oracle_writes():
+    """tests/golden/checkpoints.safetensors equals a fresh run of its generator (the CPU
+    oracle), so the GPU tests below compare against the oracle."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_checkpoints", GOLDEN.with_name("make_checkpoints.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    fresh, disk = mod.make(), _golden()
+    assert set(fresh) == set(disk)
+    for k in fresh:
+        if k.split(".")[-1].startswith("expected"):
+            # fp32 CPU matmuls: the summation order, hence the last bits, depends on the host BLAS
+            assert fresh[k].dtype == disk[k].dtype and torch.allclose(fresh[k], disk[k], rtol=1e-5, atol=1e-6), k
+        else:
+            assert _same(fresh[k], disk[k]), k
+
+
+def _load_layer(st, name, device):
+    """Rebuild a layer's weight the way the reference's loaders do: codes from `weight`, the
+    NVFP4 block scales from the flat uint8 `weight_scale` viewed as e4m3 with `weight_scale_2`
+    as the tensor scale (samples/nvfp4_linear.py:39-61); FP8 / MXFP8 scales from
+    `weight_scale` (tensor/fp8.py:74-80, tensor/mxfp8.py:86-87)."""
+    w = st["w_bf16"]
+    shape = tuple(w.shape)
+    codes = st[f"{name}.weight"].to(device)
+    if name == "nvfp4":
+        params = TensorCoreNVFP4Layout.Params(scale=st["nvfp4.weight_scale_2"].to(device), orig_dtype=w.dtype,
+                                              orig_shape=shape,
+                                              block_scale=st["nvfp4.weight_scale"].to(device).view(torch.float8_e4m3fn))
+        return QuantizedTensor(codes, LAYOUTS[name], params)
+    if name == "mxfp8":
+        params = TensorCoreMXFP8Layout.Params(scale=st["mxfp8.weight_scale"].to(device).view(torch.float8_e8m0fnu),
+                                              orig_dtype=w.dtype, orig_shape=shape)
+    else:
+        params = TensorCoreFP8Layout.Params(scale=st["fp8.weight_scale"].reshape(()).to(device), orig_dtype=w.dtype,
+                                            orig_shape=shape)
+    return QuantizedTensor(codes.view(torch.float8_e4m3fn), LAYOUTS[name], params)
+
+
+def _rel_l2(got, want):
+    return ((got.float().cpu() - want).norm() / want.norm()).item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,static", [("fp8", False), ("mxfp8", False), ("nvfp4", False), ("nvfp4", True)],
+                         ids=["fp8", "mxfp8", "nvfp4-dynamic", "nvfp4-static"])
+def test_golden_checkpoint_linear_matches_the_oracle(name, static, hip):
+    """F.linear on the GPU, with the weight loaded from the oracle-made checkpoint and the
+    activation quantized by the layout (dynamic scale, or the checkpoint's input_scale),
+    equals the oracle's result within bf16 output rounding (rel-L2 <= 1e-2)."""
+    st = _golden()
+    dev = torch.device("cuda", 0)
+    w = _load_layer(st, name, dev)
+    x = st["x"].to(dev)
+    kw = {"scale": st["nvfp4.input_scale"].to(dev)} if static else {}
+    xq = QuantizedTensor.from_float(x, LAYOUTS[name], **kw)
+    y = torch.nn.functional.linear(xq, w, st[f"{name}.bias"].to(dev))
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (x.shape[0], w.shape[0])
+    want = st[f"{name}.expected_static" if static else f"{name}.expected"]
+    assert _rel_l2(y, want) <= 4e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["fp8", "mxfp8", "nvfp4"])
+def test_golden_checkpoint_bytes_from_the_gpu_quantizers(name, hip):
+    """Quantizing the checkpoint's source weight on the GPU through the layout reproduces the
+    committed codes and scales bit for bit."""
+    st = _golden()
+    qt = QuantizedTensor.from_float(st["w_bf16"].cuda(), LAYOUTS[name])
+    sd = {k: v.cpu() for k, v in qt.state_dict("weight").items()}
+    assert torch.equal(_bits(sd["weight"]), st[f"{name}.weight"])
+    if name == "nvfp4":
+        assert torch.equal(_bits(sd["weight_scale"]).reshape(-1), st["nvfp4.weight_scale"])
+        assert torch.equal(sd["weight_scale_2"].reshape(1), st["nvfp4.weight_scale_2"])
+    elif name == "mxfp8":
+        assert torch.equal(_bits(sd["weight_scale"]), st["mxfp8.weight_scale"])
+    else:
+        assert torch.equal(sd["weight_scale"].reshape(1), st["fp8.weight_scale"])
