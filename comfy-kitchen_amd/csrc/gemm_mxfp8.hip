@@ -47,6 +47,7 @@
 #include <utility>
 
 #include "ckh_common.h"
+#include "quant_math.h"
 
 namespace ckh {
 namespace mx {
@@ -195,6 +196,78 @@ __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], u
     store_pair(L, x, tx, ty, std::make_integer_sequence<int, NP>{});
 }
 
+// 16-bit activation, quantized to MXFP8 in the load path (scaled_mm_mxfp8_dynamic): one
+// stage at a time, 64 elements = 128 bytes of each of the tile's 256 rows.  Wave w, load j
+// covers rows R = 64 w + 8 j .. +7: lane i fetches 16-byte chunk c = i % 8 (8 elements)
+// of row R + i / 8, so each 8 lanes read one whole 128-byte line and lanes 4b .. 4b+3 of
+// a row hold its 32-element block b.  The chunk's 8 E4M3 codes go to logical chunk c / 2,
+// half c % 2, of the row in the stage's activation tile (physical chunk (c/2) ^ swz(row)).
+struct Loader16 {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t voff;      // lane's global byte offset for j = 0, stage 0
+    uint32_t rowstep;   // 8 rows: global distance between consecutive loads j
+    uint32_t lds_even;  // LDS offset of the codes within a stage tile for even j (adds 512 j);
+                        // for odd j the chunk index is xor 1, i.e. the offset xor 16
+    uint32_t sc_off;    // offset of the row's scale word in the stage buffer's activation
+                        // scale area (j = 0), plus the block's byte within the stage
+};
+
+__device__ __forceinline__ Loader16 make_loader16(const uint8_t* tile_base, int valid_rows, int K, int wave,
+                                                  int lane) {
+    Loader16 L;
+    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * 2u * K);
+    const int row = 64 * wave + (lane >> 3), c = lane & 7;
+    L.voff = static_cast<uint32_t>(row * 2 * K + 16 * c);
+    L.rowstep = 16u * K;
+    L.lds_even = static_cast<uint32_t>(row * BK + ((((c >> 1) ^ swz(row))) << 4) + (c & 1) * 8);
+    // word of row R = 64 w + 8 j + i/8 in a 256-row scale chunk pair: (R/128)*512 +
+    // (R%32)*16 + ((R%128)/32)*4, and block b = c/4 of the stage's two is byte b of the
+    // stage's pair of bytes
+    L.sc_off = static_cast<uint32_t>((wave >> 1) * 512 + (lane >> 3) * 16 + (wave & 1) * 8 + (c >> 2));
+    return L;
+}
+
+// Offset added for stage s: past K the lane reads zeros from outside the descriptor.
+__device__ __forceinline__ uint32_t stage_add16(int k0, int K, int lane) {
+    return (k0 + 8 * (lane & 7) < K) ? static_cast<uint32_t>(2 * k0) : 0x80000000u;
+}
+
+template <int J>
+__device__ __forceinline__ void load_piece16(const Loader16& L, v4u (&x)[8], uint32_t add) {
+    x[J] = __builtin_amdgcn_raw_buffer_load_b128(L.rs, L.voff + J * L.rowstep + add, 0, 0);
+}
+
+// Quantize piece J (8 elements of one 32-element block) as quantize_mxfp8 does (the codes
+// and exponent of mx_codes16 but for scale-0 blocks, below; block amax over the lane quad)
+// and store its codes to the stage tile at
+// `tile`; the quad stores the block's E8M0 byte to the stage's scale area `sc` at byte
+// 2 * ODD + b of the row's word, the byte the stage's MFMAs select.
+template <int AIN, int J, bool ODD>
+__device__ __forceinline__ void quantize_piece16(const Loader16& L, const v4u (&x)[8], uint8_t* tile, uint8_t* sc,
+                                                 int lane) {
+    const uint4 w = make_uint4(x[J][0], x[J][1], x[J][2], x[J][3]);
+    uint32_t m = amax16x8(w);
+    m = max(m, dpp<0xB1>(m));  // quad_perm [1,0,3,2]
+    m = max(m, dpp<0x4E>(m));  // quad_perm [2,3,0,1]
+    const uint32_t bits = amax16_to_f32_bits<AIN>(m);
+    // Branch-free (a branch here splits the stage's hand-scheduled slots and lets the
+    // compiler sink the MFMAs past the stage barriers).  Exponent 0 is a zero block (+0
+    // codes, as quantize_mxfp8) or a scale of 0.0 (infinite amax, or a nonzero amax of at
+    // most ~1.3e-36), where quantize_mxfp8 writes 0x7E|sign / 0xFF codes whose products
+    // with scale byte 0 are +-448 * 2^-127 * b: here such a block contributes 0, or NaN
+    // codes when it holds a NaN (amax NaN), so the output keeps the NaN.
+    const uint32_t e = mx_exponent_select(bits);
+    const float scale = as_f((e ? e : 1u) << 23);
+    uint2 codes = make_uint2(scaled_e4m3x4<AIN>(w.x, w.y, scale), scaled_e4m3x4<AIN>(w.z, w.w, scale));
+    // materialised here: otherwise the compiler sinks the converts into a branch on e
+    __asm__ volatile("" : "+v"(codes.x), "+v"(codes.y));
+    const uint32_t fill = bits > 0x7f800000u ? ~0u : 0u;
+    codes = e ? codes : make_uint2(fill, fill);
+    *reinterpret_cast<uint2*>(tile + ((J & 1) ? (L.lds_even ^ 16u) : L.lds_even) + 512 * J) = codes;
+    // all four lanes of the quad store the same byte (a guard would be a branch)
+    sc[L.sc_off + (J & 3) * 128 + (J >> 2) * 4 + (ODD ? 2 : 0)] = static_cast<uint8_t>(e);
+}
+
 // Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
 // two contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
 // (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand w >> 1 (0 = weight,
@@ -307,12 +380,20 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 // 256 x 128 half tiles that finish a grid whose last round would leave most CUs idle.
 // bid: the workgroup's index among the workgroups of its kind (full or half tiles).
 //
+// AIN: -1 when the activation is E4M3 codes with E8M0 scales; CKH_BF16 / CKH_F16 when it
+// is a 16-bit tensor quantized to MXFP8 in the load path (scaled_mm_mxfp8_dynamic): each
+// stage t quantizes the activation of stage t + 2 into its buffer (codes and the E8M0
+// bytes its MFMAs select) and loads that of stage t + 3, so the activation moves one stage
+// at a time through the same 32 staging registers; every wave moves weight scale words.
+//
 // Stage buffers 0, 1 and 2, 3 live in two arrays.  Every stage reads fragments from one
 // array and writes staged data into the other, so the compiler knows they never alias
 // and may interleave the two freely; within an array, per-lane addresses of different
 // buffers differ only by immediates.
-template <int OUT, int BIAS, bool UNIT, int NW>
+template <int OUT, int BIAS, bool UNIT, int NW, int AIN>
 __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01, uint8_t* lds23) {
+    constexpr bool AQ = AIN >= 0;
+    static_assert(!(AQ && UNIT), "the in-load quantize produces block scales");
     constexpr int TBN = 64 * NW;  // tile width along n
     constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
     constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
@@ -335,6 +416,11 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
 
     const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * p.K, min(TBN, p.N - n0), p.K, wave, lane, TBN / 4);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * p.K, min(BM, p.M - m0), p.K, wave, lane);
+    const Loader16 LA16 = make_loader16(p.a + static_cast<int64_t>(m0) * 2 * p.K, min(BM, p.M - m0), p.K, wave, lane);
+    // scale words: waves 0, 1 move the weight's, waves 2, 3 the activation's; with the
+    // in-load quantize, waves 2, 3 repeat waves 0, 1 (identical bytes to the same LDS
+    // words: a branch instead would let the compiler sink the MFMAs past the barriers)
+    const int swave = AQ ? (wave & 1) : wave;
     const __amdgpu_buffer_rsrc_t rssb = make_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = make_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
@@ -357,7 +443,20 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     ScaleWords SW;
     auto load_b = [&](int s) {
         load_pair<PB>(LB, SB, s * BK, p.K);
-        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
+        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, swave, lane);
+    };
+    // the activation of stage s into x (16-bit path)
+    auto load_a16 = [&](v4u (&x)[8], int s) {
+        const uint32_t add = stage_add16(s * BK, p.K, lane);
+        for_each_index([&](auto j_c) { load_piece16<decltype(j_c)::value>(LA16, x, add); },
+                       std::make_integer_sequence<int, 8>{});
+    };
+    // quantize the staged activation x of stage s (parity ODD) into buffer b_c
+    auto quantize_a16 = [&](const v4u (&x)[8], auto b_c, auto odd_c) {
+        for_each_index([&](auto j_c) {
+            quantize_piece16<AIN, decltype(j_c)::value, decltype(odd_c)::value>(LA16, x, buf(b_c) + TILE,
+                                                                                buf(b_c) + 2 * TILE + STILE, lane);
+        }, std::make_integer_sequence<int, 8>{});
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
@@ -408,6 +507,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         uint8_t* wx = EVEN ? buf(P2{}) : buf(P3{}) + TILE;
         uint8_t* wy = EVEN ? buf(P3{}) : buf(b_c) + TILE;
         const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, p.K) : pair_add(LB, (t + 3) * BK, p.K);
+        const uint32_t add16 = stage_add16((t + 3) * BK, p.K, lane);
         v4u wb, wa;
         uint32_t nb[4], na[4];
         auto slot = [&](auto k_c) {
@@ -423,7 +523,14 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
             if constexpr (k == 2) G.b[0] = read_frag(nx, fab);
             if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
             if constexpr (k >= 6 && k <= 4 + NW) G.b[k - 5] = read_frag(nx + (k - 5) * 32 * BK, fab);
-            if constexpr (k < 8) {
+            if constexpr (k < 8 && AQ) {
+                quantize_piece16<AIN, k, !EVEN>(LA16, SA, buf(P2{}) + TILE, buf(P2{}) + 2 * TILE + STILE, lane);
+                load_piece16<k>(LA16, SA, add16);
+                if constexpr (k < PB) {
+                    if constexpr (EVEN) store_piece<k>(LB, SB, wx, wy);
+                    else load_piece<k>(LB, SB, add);
+                }
+            } else if constexpr (k < 8) {
                 if constexpr (EVEN) {
                     if constexpr (k < PB) store_piece<k>(LB, SB, wx, wy);
                     load_piece<k>(LA, SA, add);
@@ -433,8 +540,8 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
                 }
             }
             if constexpr (k == (SLOTS > 8 ? 8 : SLOTS - 1) && !UNIT) {
-                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
-                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
+                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, swave, lane);
+                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, swave, lane);
             }
             if constexpr (k == SLOTS - 4) {
 #pragma unroll
@@ -461,7 +568,22 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // prologue: stages 0..3 resident except the weight half of 2, 3 (staged in SB for
     // stage 0 to write), stage 0 read.  All four pairs are loaded before the first LDS
     // write, so the prologue waits out one memory latency rather than two.
-    {
+    if constexpr (AQ) {
+        // activation stages 0, 1 quantized into their buffers, stage 2 staged in SA for
+        // stage 0 to quantize; weight as below
+        v4u XA[8], X1[8], XB[8];
+        ScaleWords XW;
+        load_a16(XA, 0);
+        load_a16(X1, 1);
+        load_pair<PB>(LB, XB, 0, p.K);
+        load_scales(XW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, 0, p.K, swave, lane);
+        load_b(2);
+        load_a16(SA, 2);
+        quantize_a16(XA, B0{}, std::false_type{});
+        quantize_a16(X1, B1{}, std::true_type{});
+        store_pair<PB>(LB, XB, buf(B0{}), buf(B1{}));
+        store_scales(XW, buf(B0{}) + 2 * TILE, buf(B1{}) + 2 * TILE, swave, lane);
+    } else {
         v4u XA[8], XB[8];
         ScaleWords XW;
         load_a(0);
@@ -574,13 +696,13 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
 // The dispatcher starts half-tile workgroups on CUs as their last full tile ends, so
 // the tail overlaps the uneven end of the previous round instead of waiting for a
 // second launch.
-template <int OUT, int BIAS, bool UNIT>
+template <int OUT, int BIAS, bool UNIT, int AIN>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
     const int b = blockIdx.x;
-    if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4>(p, b, lds01, lds23);
-    else gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
+    if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4, AIN>(p, b, lds01, lds23);
+    else gemm_tile<OUT, BIAS, UNIT, 2, AIN>(p, b - p.n_full, lds01, lds23);
 }
 
 }  // namespace mx
@@ -593,15 +715,18 @@ namespace {
 // Workgroups that can hold a 256 x 256 tile at once: one per CU.
 constexpr int kGemmSlots = 256;
 
-template <bool UNIT>
+// The 16-bit-activation kernels take a bias of the output's dtype only (as the layouts
+// pass it), which keeps their instantiations to three per activation dtype.
+template <bool UNIT, int AIN>
 void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT>), dim3(wgs), dim3(mx::NT), 0, st, p)
-#define BY_BIAS(O)                                         \
-    do {                                                   \
-        if (!has_bias) LAUNCH(O, -1);                      \
-        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
-        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
-        else LAUNCH(O, CKH_BF16);                          \
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT, AIN>), dim3(wgs), dim3(mx::NT), 0, st, p)
+#define BY_BIAS(O)                                                     \
+    do {                                                               \
+        if (!has_bias) LAUNCH(O, -1);                                  \
+        else if constexpr (AIN >= 0) LAUNCH(O, O);                     \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32);             \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16);             \
+        else LAUNCH(O, CKH_BF16);                                      \
     } while (0)
     if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
     else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
@@ -613,14 +738,14 @@ void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, b
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
 // half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
 // half tiles (about 55% of a full tile's time each), in the same grid.
-template <bool UNIT>
+template <bool UNIT, int AIN = -1>
 int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
     const int tiles = p.tiles_m * p.tiles_n;
     const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : 0;
     p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
     p.n_full = tiles - p.n_half;
-    launch_grid<UNIT>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
-    return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
+    launch_grid<UNIT, AIN>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
+    return check_launch(UNIT ? "scaled_mm_fp8" : AIN >= 0 ? "scaled_mm_mxfp8_dynamic" : "scaled_mm_mxfp8");
 }
 
 mx::Args base_args(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N, int64_t K) {
@@ -682,4 +807,32 @@ extern "C" int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scal
     p.tsa = scale_a;
     p.tsb = scale_b;
     return launch_gemm<true>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int ckh_scaled_mm_mxfp8_dynamic(const void* a, const void* b, const void* sb, const void* bias, void* out,
+                                           int64_t M, int64_t N, int64_t K, int a_code, int out_code, int bias_code,
+                                           uintptr_t stream) {
+    CKH_REQUIRE(a && b && sb && out, "scaled_mm_mxfp8_dynamic: null pointer");
+    CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_mxfp8_dynamic: sizes must be M, N >= 0 and K > 0");
+    CKH_REQUIRE(K % 32 == 0, "scaled_mm_mxfp8_dynamic: K (%lld) must be a multiple of 32", (long long)K);
+    CKH_REQUIRE(a_code == CKH_BF16 || a_code == CKH_F16,
+                "scaled_mm_mxfp8_dynamic: unsupported activation dtype code %d (bf16 or f16)", a_code);
+    CKH_REQUIRE(2 * M * K < (1ll << 31) && N * K < (1ll << 31) && K < (1ll << 24),
+                "scaled_mm_mxfp8_dynamic: operand larger than 2 GiB");
+    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
+                "scaled_mm_mxfp8_dynamic: unsupported output dtype code %d", out_code);
+    CKH_REQUIRE(!bias || bias_code == out_code,
+                "scaled_mm_mxfp8_dynamic: bias dtype code %d must be the output's (%d)", bias_code, out_code);
+    CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sb, 4) && aligned(out, 16),
+                "scaled_mm_mxfp8_dynamic: pointers misaligned");
+    if (M == 0 || N == 0) return CKH_OK;
+    mx::Args p = base_args(a, b, bias, out, M, N, K);
+    p.sa = static_cast<const uint8_t*>(sb);  // unused: the activation's scales are made in the kernel
+    p.sb = static_cast<const uint8_t*>(sb);
+    p.ncb = static_cast<int>(cdiv(K / 32, 4));
+    p.sa_rows = 0;
+    p.sb_rows = static_cast<int>(rup(N, 128));
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (a_code == CKH_BF16) return launch_gemm<false, CKH_BF16>(p, out_code, bias_code, bias != nullptr, st);
+    return launch_gemm<false, CKH_F16>(p, out_code, bias_code, bias != nullptr, st);
 }

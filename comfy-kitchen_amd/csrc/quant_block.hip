@@ -47,31 +47,6 @@ __device__ __forceinline__ uint32_t absmax_bits(const float (&v)[8]) {
 }
 
 // ------------------------------------------------------------------- MXFP8
-// Codes for one lane's 8 values given the block's amax bits and exponent.
-__device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_bits, uint32_t e) {
-    uint32_t w[2] = {0u, 0u};
-    if (amax_bits == 0) return make_uint2(0u, 0u);  // zero block: +0 codes
-    if (e == 0) {
-        // Scale 0.0: x/0 is +-inf (clamped to +-448) for x != 0 and NaN for x == 0.
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            uint32_t a = as_u(v[t]) & 0x7fffffffu;
-            uint32_t c = (a == 0 || a > 0x7f800000u) ? 0xffu : (0x7eu | ((as_u(v[t]) >> 24) & 0x80u));
-            w[t >> 2] |= c << (8 * (t & 3));
-        }
-        return make_uint2(w[0], w[1]);
-    }
-    // x / 2^(e-127) == x * 2^(127-e) exactly (both correctly rounded); 1 <= e <= 254
-    // keeps 2^(127-e) a normal float.  Here amax is finite and 2^(e-127) >= amax/448, so
-    // every |q| <= 448: the reference's clamp is a no-op and the hardware convert
-    // (RNE, identical to f_to_e4m3 on this range) encodes directly.
-    const float mul = as_f((254u - e) << 23);
-    float q[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) q[t] = v[t] * mul;
-    return make_uint2(hw_e4m3x4(q[0], q[1], q[2], q[3]), hw_e4m3x4(q[4], q[5], q[6], q[7]));
-}
-
 template <int IN>
 __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __restrict__ x,
                                                                   uint8_t* __restrict__ qx,
@@ -117,37 +92,6 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_kernel(const void* __
 //   * the scale word is OR-combined with two DPP row_ror steps.
 // Blocks whose amax is zero, tiny (biased exponent < 10) or non-finite take the
 // general encoder.
-
-__device__ __forceinline__ uint32_t amax16x8(uint4 w) {
-    auto h = [](uint32_t v) { return __builtin_bit_cast(ckh_u16x2, v & 0x7fff7fffu); };
-    ckh_u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(h(w.x), h(w.y)),
-                                            __builtin_elementwise_max(h(w.z), h(w.w)));
-    return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y));
-}
-
-
-// 16-bit amax bits -> fp32 bits of the same value
-template <int IN>
-__device__ __forceinline__ uint32_t amax16_to_f32_bits(uint32_t m) {
-    if constexpr (IN == CKH_BF16) return m << 16;
-    else return as_u(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(m))));
-}
-
-template <int IN>
-__device__ __forceinline__ void unpack16x8(uint4 w, float (&v)[8]) {
-    const uint32_t p[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if constexpr (IN == CKH_BF16) {
-            v[2 * i] = as_f(p[i] << 16);
-            v[2 * i + 1] = as_f(p[i] & 0xffff0000u);
-        } else {
-            ckh_f16x2 h = __builtin_bit_cast(ckh_f16x2, p[i]);
-            v[2 * i] = static_cast<float>(h.x);
-            v[2 * i + 1] = static_cast<float>(h.y);
-        }
-    }
-}
 
 // Work mapping of the fast kernels.  The swizzled scale words of the units in one
 // 128-row tile and one unit column j form a contiguous 512-byte span, but neighbouring
@@ -204,17 +148,7 @@ __global__ __launch_bounds__(kThreads) void quantize_mxfp8_fast_kernel(const uin
         m = max(m, dpp<0x4E>(m));  // quad_perm [2,3,0,1]
         const uint32_t bits = amax16_to_f32_bits<IN>(m);
         uint32_t e;
-        uint2 codes;
-        if (bits >= (10u << 23) && bits < 0x7f800000u) {
-            e = (bits >> 23) - 8u + ((bits & 0x7fffffu) > 0x600000u);
-            const float scale = as_f(e << 23);
-            codes = make_uint2(scaled_e4m3x4<IN>(w[u].x, w[u].y, scale), scaled_e4m3x4<IN>(w[u].z, w[u].w, scale));
-        } else {
-            e = mx_exponent(bits);
-            float v[8];
-            unpack16x8<IN>(w[u], v);
-            codes = mx_encode8(v, bits, e);
-        }
+        const uint2 codes = mx_codes16<IN>(w[u], bits, e);
         if (r[u] < rows) *reinterpret_cast<uint2*>(qx + off[u]) = codes;
         uint32_t word = e << (8 * (l >> 2));
         word |= dpp<0x124>(word);  // row_ror:4

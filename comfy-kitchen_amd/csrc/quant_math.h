@@ -51,6 +51,128 @@ __device__ __forceinline__ uint32_t scaled_e4m3x4(uint32_t a, uint32_t b, float 
     return __builtin_bit_cast(uint32_t, o);
 }
 
+// Codes for one lane's 8 values given the block's amax bits and exponent.
+__device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_bits, uint32_t e) {
+    uint32_t w[2] = {0u, 0u};
+    if (amax_bits == 0) return make_uint2(0u, 0u);  // zero block: +0 codes
+    if (e == 0) {
+        // Scale 0.0: x/0 is +-inf (clamped to +-448) for x != 0 and NaN for x == 0.
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t a = as_u(v[t]) & 0x7fffffffu;
+            uint32_t c = (a == 0 || a > 0x7f800000u) ? 0xffu : (0x7eu | ((as_u(v[t]) >> 24) & 0x80u));
+            w[t >> 2] |= c << (8 * (t & 3));
+        }
+        return make_uint2(w[0], w[1]);
+    }
+    // x / 2^(e-127) == x * 2^(127-e) exactly (both correctly rounded); 1 <= e <= 254
+    // keeps 2^(127-e) a normal float.  Here amax is finite and 2^(e-127) >= amax/448, so
+    // every |q| <= 448: the reference's clamp is a no-op and the hardware convert
+    // (RNE, identical to f_to_e4m3 on this range) encodes directly.
+    const float mul = as_f((254u - e) << 23);
+    float q[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) q[t] = v[t] * mul;
+    return make_uint2(hw_e4m3x4(q[0], q[1], q[2], q[3]), hw_e4m3x4(q[4], q[5], q[6], q[7]));
+}
+
+// |x| maxima of 8 packed 16-bit values as a 16-bit integer (orders like the values).
+__device__ __forceinline__ uint32_t amax16x8(uint4 w) {
+    auto h = [](uint32_t v) { return __builtin_bit_cast(ckh_u16x2, v & 0x7fff7fffu); };
+    ckh_u16x2 m = __builtin_elementwise_max(__builtin_elementwise_max(h(w.x), h(w.y)),
+                                            __builtin_elementwise_max(h(w.z), h(w.w)));
+    return max(static_cast<uint32_t>(m.x), static_cast<uint32_t>(m.y));
+}
+
+
+// 16-bit amax bits -> fp32 bits of the same value
+template <int IN>
+__device__ __forceinline__ uint32_t amax16_to_f32_bits(uint32_t m) {
+    if constexpr (IN == CKH_BF16) return m << 16;
+    else return as_u(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(m))));
+}
+
+template <int IN>
+__device__ __forceinline__ void unpack16x8(uint4 w, float (&v)[8]) {
+    const uint32_t p[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (IN == CKH_BF16) {
+            v[2 * i] = as_f(p[i] << 16);
+            v[2 * i + 1] = as_f(p[i] & 0xffff0000u);
+        } else {
+            ckh_f16x2 h = __builtin_bit_cast(ckh_f16x2, p[i]);
+            v[2 * i] = static_cast<float>(h.x);
+            v[2 * i + 1] = static_cast<float>(h.y);
+        }
+    }
+}
+
+// Codes of one lane's 8 packed 16-bit values w (E4M3) and the E8M0 exponent e of their
+// 32-element block, whose amax has fp32 bits `bits`: the packed scaled convert on the
+// common range, the general encoder for zero, tiny and non-finite blocks.  This is the
+// MXFP8 quantizer's step; the bf16-activation GEMM calls it too, so both produce the same
+// codes and scales.
+template <int IN>
+__device__ __forceinline__ uint2 mx_codes16(uint4 w, uint32_t bits, uint32_t& e) {
+    if (bits >= (10u << 23) && bits < 0x7f800000u) {
+        e = (bits >> 23) - 8u + ((bits & 0x7fffffu) > 0x600000u);
+        const float scale = as_f(e << 23);
+        return make_uint2(scaled_e4m3x4<IN>(w.x, w.y, scale), scaled_e4m3x4<IN>(w.z, w.w, scale));
+    }
+    e = mx_exponent(bits);
+    float v[8];
+    unpack16x8<IN>(w, v);
+    return mx_encode8(v, bits, e);
+}
+
+// The codes of a block whose scale is 0.0 (exponent 0 with a nonzero amax: a tiny or
+// non-finite amax): x / 0 is +-inf, clamped to 0x7E | sign, for a nonzero non-NaN x, and
+// NaN, 0xFF, for x = +-0 or NaN.  Straight-line bit operations.
+template <int IN>
+__device__ __forceinline__ uint2 mx_codes16_scale0(uint4 w) {
+    constexpr uint32_t kInf = IN == CKH_BF16 ? 0x7f80u : 0x7c00u;
+    const uint32_t h[4] = {w.x, w.y, w.z, w.w};
+    uint32_t c[2] = {0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint32_t x = (h[t >> 1] >> (16 * (t & 1))) & 0xffffu, a = x & 0x7fffu;
+        const uint32_t code = (a == 0 || a > kInf) ? 0xffu : (0x7eu | ((x >> 8) & 0x80u));
+        c[t >> 2] |= code << (8 * (t & 3));
+    }
+    return make_uint2(c[0], c[1]);
+}
+
+// mx_codes16 with no float arrays or software encoders, for callers with no registers to
+// spare (the bf16-activation GEMM): the same codes and exponent for every input.  With e =
+// mx_exponent(amax) >= 1 the scale 2^(e-127) >= amax/448 is normal and the scaled convert
+// equals the reference's x / scale -> E4M3 (the MXFP8 hardware identity); e == 0 means a
+// zero block (+0 codes), or a scale of 0.0 (tiny or non-finite amax), for which x / 0
+// gives 0x7E | sign for a nonzero non-NaN x (clamped +-inf) and 0xFF for 0 or NaN.
+template <int IN>
+__device__ __forceinline__ uint2 mx_codes16_compact(uint4 w, uint32_t bits, uint32_t& e) {
+    e = mx_exponent(bits);
+    if (e != 0) {
+        const float scale = as_f(e << 23);
+        return make_uint2(scaled_e4m3x4<IN>(w.x, w.y, scale), scaled_e4m3x4<IN>(w.z, w.w, scale));
+    }
+    if (bits == 0) return make_uint2(0u, 0u);
+    return mx_codes16_scale0<IN>(w);
+}
+
+// mx_exponent without branches (the same value for every input): the closed form on the
+// common range, 0 for non-finite amax, and for amax below 2^-117 (biased exponent < 10)
+// two thresholds: the division form s = RN(amax / 448) gives e = 0 up to amax bits
+// 0x04600001 (s <= 2^-127), 1 up to 0x04E00000 (s <= 2^-126) and 2 above (s < 2^-125),
+// found by evaluating it on every such amax.
+__device__ __forceinline__ uint32_t mx_exponent_select(uint32_t bits) {
+    uint32_t fast = (bits >> 23) - 8u + ((bits & 0x7fffffu) > 0x600000u);
+    uint32_t tiny = (bits > 0x04600001u ? 1u : 0u) + (bits > 0x04e00000u ? 1u : 0u);
+    // both materialised, so the compiler keeps the selects (no branch on the range)
+    __asm__ volatile("" : "+v"(fast), "+v"(tiny));
+    return bits >= 0x7f800000u ? 0u : (bits >= (10u << 23) ? fast : tiny);
+}
+
 // Pack 8 non-NaN values into E2M1 nibbles with the hardware convert: RNE, identical to
 // f_to_e2m1 of the value clamped to [-6, 6] (the convert saturates), and the first
 // operand lands in the low nibble.
