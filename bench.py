@@ -205,6 +205,8 @@ def bench_lib():
         lib.ckh_bench_copy_floor.restype = ctypes.c_int
         lib.ckh_bench_copy_floor.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
                                              ctypes.c_uint64]
+        lib.ckh_bench_mfma_loop.restype = ctypes.c_int
+        lib.ckh_bench_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_uint64]
         _bench_lib = lib
     return _bench_lib
 
@@ -252,7 +254,8 @@ def roofline_flops(flops, ms, peak, traffic=None):
 
 
 def load_traffic() -> dict:
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), if recorded."""
+    """Bytes per launch that missed L2, measured with rocprofv3 --pmc (TCC FETCH_SIZE + WRITE_SIZE), if
+    recorded: HBM traffic plus Infinity-Cache (MALL) hits, i.e. an upper bound on HBM bytes."""
     p = REPO / "profiles" / "traffic.json"
     if p.exists():
         try:
@@ -517,10 +520,15 @@ def run_cpu_baseline(configs, log):
 
 # ------------------------------------------------------------------ PMC traffic
 # `--pmc-driver` makes the dispatch sequence that two rocprofv3 --pmc passes count
-# (FETCH_SIZE, then WRITE_SIZE); `--summarize-pmc` turns them into HBM bytes per launch
+# (FETCH_SIZE, then WRITE_SIZE); `--summarize-pmc` turns them into L2-miss bytes per launch
+# (what the L2s fetch from and write to the fabric: HBM plus Infinity-Cache hits)
 # in profiles/traffic.json, which the roofline lines report as `traffic`.
 PMC_CALLS = 3
 PMC_CALIB_BYTES = 256 << 20
+PMC_MFMA_ITERS = 4000  # 64,000 MFMAs per wave, ~2 ms
+# the one-pass SQ counter set of `--summarize-counters` (at most 8 SQ counters per pass)
+SQ_COUNTERS = ("SQ_WAVES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
+               "SQ_LDS_BANK_CONFLICT SQ_LDS_ADDR_CONFLICT")
 
 
 def pmc_sequence(configs, dev):
@@ -558,13 +566,18 @@ def pmc_sequence(configs, dev):
 
 
 def pmc_driver(configs):
-    """One calibration kernel (negate 256 MiB of fp32: reads and writes PMC_CALIB_BYTES), then
-    PMC_CALLS eager calls of each op; no hipMemset/copy between them."""
+    """The MFMA-busy calibration loop (one workgroup per CU), one traffic calibration kernel
+    (negate 256 MiB of fp32: reads and writes PMC_CALIB_BYTES), then PMC_CALLS eager calls
+    of each op; no hipMemset/copy between them."""
     dev = torch.device("cuda", 0)
     seq = pmc_sequence(configs, dev)
     src = torch.ones(PMC_CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cus * 256, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
+    assert bench_lib().ckh_bench_mfma_loop(sink.data_ptr(), cus, PMC_MFMA_ITERS,
+                                           torch.cuda.current_stream().cuda_stream) == 0
     torch.neg(src, out=dst)
     for _, fn in seq:
         for _ in range(PMC_CALLS):
@@ -596,9 +609,10 @@ OP_KERNELS = {"quantize_per_tensor_fp8": "ckh::quantize_fp8", "dequantize_per_te
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str, configs, command: str):
-    """HBM bytes per launch of each op: counter KiB scaled by calibration bytes / calibration KiB."""
+    """L2-miss bytes per launch of each op: counter KiB scaled by calibration bytes / calibration KiB."""
     seq = [n for n, _ in pmc_sequence_names(configs)]
-    out = {"bytes_per_launch": {}, "calibration": {}, "command": command}
+    out = {"what": "bytes per launch that missed L2 (TCC FETCH_SIZE, WRITE_SIZE): HBM traffic plus Infinity-Cache "
+                   "hits, an upper bound on HBM bytes", "bytes_per_launch": {}, "calibration": {}, "command": command}
     for key, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
         rows = _pmc_dispatches(Path(d), counter)
         # calibration: the largest non-ckh dispatch; the measured sequence follows it
@@ -624,6 +638,69 @@ def summarize_pmc(fetch_dir: str, write_dir: str, configs, command: str):
     (REPO / "profiles").mkdir(exist_ok=True)
     (REPO / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out, indent=1))
+
+
+def summarize_counters(sq_dir: str, configs, command: str):
+    """MFMA busy and LDS conflicts per op from one rocprofv3 --pmc pass over SQ_COUNTERS.
+
+    MFMA busy = (SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES) of the op's dispatch divided by
+    the same ratio of the calibration loop, which keeps every SIMD's matrix core busy (the
+    MFMA counter sums over SIMDs, SQ_BUSY_CYCLES over shader engines).  Writes
+    profiles/counters.json and prints a markdown table."""
+    import csv
+
+    disp = {}
+    for f in sorted(Path(sq_dir).rglob("*counter_collection.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                e = disp.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])
+                e[1][r["Counter_Name"]] = e[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    rows = [(i, *disp[i]) for i in sorted(disp)]
+    ci = next(i for i, r in enumerate(rows) if "mfma_loop_kernel" in r[1])
+    cal = rows[ci][2]
+    full = cal["SQ_VALU_MFMA_BUSY_CYCLES"] / cal["SQ_BUSY_CYCLES"]
+    ours = [r for r in rows[ci + 1:] if "ckh::" in r[1]]
+    out = {"command": command, "calibration": {"kernel": rows[ci][1][:60], "mfma_busy_per_sq_busy": round(full, 3)},
+           "ops": {}}
+    i = 0
+    for name, _ in pmc_sequence_names(configs):
+        sub, run = OP_KERNELS[name], []
+        cap = PMC_CALLS if name.startswith("apply_rope") else len(ours)
+        while i < len(ours) and sub in ours[i][1] and len(run) < cap:
+            run.append(ours[i])
+            i += 1
+        assert run, f"no dispatches of {name} in the counter run"
+        kern = {}
+        for _, k, c in run:
+            acc = kern.setdefault(k, {"n": 0})
+            acc["n"] += 1
+            for cn, v in c.items():
+                acc[cn] = acc.get(cn, 0.0) + v
+        for k, acc in kern.items():
+            n = acc.pop("n")
+            mean = {cn: v / n for cn, v in acc.items()}
+            lds = max(mean.get("SQ_INSTS_LDS", 0.0), 1.0)
+            out["ops"].setdefault(name, []).append({
+                "kernel": k[:80], "dispatches": n,
+                "mfma_busy": round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / mean["SQ_BUSY_CYCLES"] / full, 4),
+                "lds_bank_conflict_cycles_per_lds_inst": round(mean.get("SQ_LDS_BANK_CONFLICT", 0.0) / lds, 4),
+                "valu_insts_per_mfma": (round(mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"], 2)
+                                        if mean.get("SQ_INSTS_MFMA") else None),
+                **{cn: round(v) for cn, v in sorted(mean.items())}})
+    (REPO / "profiles").mkdir(exist_ok=True)
+    (REPO / "profiles" / "counters.json").write_text(json.dumps(out, indent=1) + "\n")
+    print(f"calibration ({out['calibration']['kernel']}): SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES = {full:.3f}")
+    print("| op | kernel | MFMA busy | LDS bank-conflict cycles | LDS address conflicts | LDS insts | MFMA insts | "
+          "VALU insts per MFMA |")
+    print("|---|---|---|---|---|---|---|---|")
+    for name, ks in out["ops"].items():
+        for e in ks:
+            has_mfma = e["valu_insts_per_mfma"] is not None
+            busy = f"{100 * e['mfma_busy']:.1f}%" if has_mfma else "-"
+            ratio = e["valu_insts_per_mfma"] if has_mfma else "-"
+            print(f"| {name} | `{e['kernel'][:48]}` | {busy} | {e.get('SQ_LDS_BANK_CONFLICT', 0):,} | "
+                  f"{e.get('SQ_LDS_ADDR_CONFLICT', 0):,} | {e.get('SQ_INSTS_LDS', 0):,} | {e.get('SQ_INSTS_MFMA', 0):,} | "
+                  f"{ratio} |")
 
 
 def pmc_sequence_names(configs):
@@ -652,9 +729,14 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc output directories")
     ap.add_argument("--pmc-command", default="", help="command recorded in profiles/traffic.json")
+    ap.add_argument("--summarize-counters", metavar="SQ_DIR",
+                    help="write profiles/counters.json (MFMA busy, LDS conflicts) from a rocprofv3 --pmc pass "
+                         "over SQ_COUNTERS")
     args = ap.parse_args()
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc, set(args.configs.split(",")), args.pmc_command)
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters, set(args.configs.split(",")), args.pmc_command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -680,6 +762,7 @@ def main():
     primary = "quantize_mxfp8" if "quantize_mxfp8" in gpu else next(iter(gpu))
     p = gpu[primary]
     roof = {k: p[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    roof["traffic_counts"] = "L2-miss bytes per launch (TCC FETCH_SIZE + WRITE_SIZE): HBM plus Infinity-Cache hits"
     line = {
         "metric": METRIC,
         "value": p["achieved"],
