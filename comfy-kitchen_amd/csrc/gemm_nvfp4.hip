@@ -27,12 +27,18 @@
 // Within a stage each lane needs, per 32-row tile, 16 bytes (32 codes: k = 32h ..
 // 32h+31 of the stage for lane half h, of which MFMA substep kk uses bytes 4kk..4kk+3)
 // and the tile row's scale word (blocks 2h and 2h+1 are its); one ds_read_b128 each.
-// The decode of substep kk+1 (VALU, independent of the MFMAs in flight) is placed by
-// the compiler's scheduler between the 16 MFMAs of substep kk.
+// Each of a substep's 16 MFMAs sits in a slot of its own (sched_barrier) with 1/16 of
+// the next substep's decode (two converts, two packed multiplies), and in the first
+// substep one of the next stage's 10 LDS reads and, in the last stage of a group, one
+// of the 18 loads of the group after next.  A 32-cycle f16 MFMA hides about 8 such
+// VALU instructions; left to itself the compiler clustered the decode between runs of
+// back-to-back MFMAs, which kept the matrix cores 60% busy instead of 77%.
 //
 // LDS rows are 128 bytes (a group); logical 16-byte chunk c of row r is stored at
-// chunk c ^ (r & 7), so the 32 rows of a fragment read hit distinct banks.  Workgroups
-// walk the tiles XCD-contiguously in grouped order, as in the MXFP8 kernel.
+// chunk c ^ (r & 7) ^ ((r >> 3) & 1), so any 16 consecutive rows of a fragment read
+// hit distinct banks of the 64-bank LDS (measured: no bank conflicts; with c ^ (r & 7)
+// rows r and r + 8 collided).  Workgroups walk the tiles XCD-contiguously in grouped
+// order, as in the MXFP8 kernel.
 #include <type_traits>
 #include <utility>
 
@@ -58,6 +64,12 @@ constexpr int GBUF = 2 * TILE + 2 * STILE;  // one group buffer: b codes, a code
 constexpr int EPI_ROW = 520;                // bytes of one staged 16-bit output row (512 + 8 pad)
 static_assert(128 * EPI_ROW <= GBUF, "half the output tile must fit one group buffer");
 constexpr int LOADS_PER_GROUP = 18;         // per wave: 8 + 8 code loads, 2 scale loads
+
+// fn(integral_constant<int, K>) for each K in order
+template <typename Fn, int... K>
+__device__ __forceinline__ void for_each_index(Fn&& fn, std::integer_sequence<int, K...>) {
+    (fn(std::integral_constant<int, K>{}), ...);
+}
 
 // s_waitcnt immediate: vmcnt in [3:0] and [15:14], expcnt [6:4] (left at 7), lgkmcnt 0
 constexpr int waitcnt_vm_lgkm0(int vm) { return (vm & 15) | (7 << 4) | ((vm >> 4) << 14); }
@@ -97,11 +109,13 @@ struct Args {
 
 // Direct-to-LDS loads of one operand's group.  Wave w, load j (0..7) covers rows
 // R = 64 w + 8 j .. +7 (1 KB of LDS); lane i fills row R + i/8, physical chunk i%8,
-// which holds logical chunk (i%8) ^ (i/8) (R is a multiple of 8).
+// which holds logical chunk (i%8) ^ (i/8) ^ (j & 1) (R is a multiple of 8, and bit 3
+// of the row is j's lowest bit).
 struct Loader {
     __amdgpu_buffer_rsrc_t rs;
     uint32_t voff;     // lane's byte offset for j = 0 and group 0
-    int cbyte;         // 16 * logical chunk
+    int cbyte;         // 16 * logical chunk for even j
+    uint32_t cdelta;   // byte offset of odd j's chunk relative to even j's (+-16)
     uint32_t rowstep;  // 8 rows
 };
 
@@ -110,17 +124,23 @@ __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int vali
     L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * Kb);
     const int row = 64 * wave + (lane >> 3);
     L.cbyte = ((lane & 7) ^ (lane >> 3)) << 4;
+    L.cdelta = static_cast<uint32_t>((L.cbyte ^ 16) - L.cbyte);
     L.voff = static_cast<uint32_t>(row * Kb + L.cbyte);
     L.rowstep = 8u * Kb;
     return L;
 }
 
+// Load j (0..7) of issue_codes alone.
+__device__ __forceinline__ void issue_code_part(const Loader& L, uint8_t* dst, int wave, int kb0, int Kb, int j) {
+    const int cb = (j & 1) ? (L.cbyte ^ 16) : L.cbyte;
+    const uint32_t add = (kb0 + cb < Kb) ? static_cast<uint32_t>(kb0) : 0x80000000u;  // past K: zeros
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + (64 * wave + 8 * j) * GKB), 16,
+                                             L.voff + j * L.rowstep + ((j & 1) ? L.cdelta : 0) + add, 0, 0, 0);
+}
+
 __device__ __forceinline__ void issue_codes(const Loader& L, uint8_t* dst, int wave, int kb0, int Kb) {
-    const uint32_t add = (kb0 + L.cbyte < Kb) ? static_cast<uint32_t>(kb0) : 0x80000000u;  // past K: zeros
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + (64 * wave + 8 * j) * GKB), 16,
-                                                 L.voff + j * L.rowstep + add, 0, 0, 0);
+    for (int j = 0; j < 8; ++j) issue_code_part(L, dst, wave, kb0, Kb, j);
 }
 
 // Scale words of a group: for a 256-row tile, 128-row block rb and word column c, the
@@ -130,12 +150,13 @@ __device__ __forceinline__ void issue_codes(const Loader& L, uint8_t* dst, int w
 // last (ncb) and blocks past the padded rows arrive as zeros.  Inside a chunk row r's
 // word sits at (r % 32) * 16 + ((r % 128) / 32) * 4.
 __device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a, int rb0_b,
-                                             int rb0_a, int ncb, int g, uint8_t* sdst, int wave, int lane) {
+                                             int rb0_a, int ncb, int g, uint8_t* sdst, int wave, int lane,
+                                             int q0 = 0, int q1 = 2) {
     const int op = wave >> 1, rb = wave & 1;
     const __amdgpu_buffer_rsrc_t rs = op ? rs_a : rs_b;
     const int base = (op ? rb0_a : rb0_b) + rb;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = q0; q < q1; ++q) {
         const int col = GS * g + 2 * q + (lane >> 5);
         const uint32_t off =
             col < ncb ? static_cast<uint32_t>((base * ncb + col) * 512 + (lane & 31) * 16) : 0x80000000u;
@@ -222,44 +243,67 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
         issue_codes(LA, d + TILE, wave, g * GKB, Kb);
         issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, g, d + 2 * TILE, wave, lane);
     };
+    // load I (0..17) of issue_group: weight codes 0..7, activation codes 8..15, scales 16, 17
+    auto issue_part = [&](auto g_c, int g, auto i_c) {
+        constexpr int I = decltype(i_c)::value;
+        uint8_t* d = gbuf(g_c);
+        if constexpr (I < 8) issue_code_part(LB, d, wave, g * GKB, Kb, I);
+        else if constexpr (I < 16) issue_code_part(LA, d + TILE, wave, g * GKB, Kb, I - 8);
+        else issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, g, d + 2 * TILE, wave, lane, I - 16, I - 15);
+    };
 
     // lane's fragment and scale-word addresses inside a group buffer
-    const int x7 = r32 & 7;
+    const int x7 = (r32 & 7) ^ ((r32 >> 3) & 1);
     const uint32_t frow_b = static_cast<uint32_t>((wn * 128 + r32) * GKB);
     const uint32_t frow_a = static_cast<uint32_t>(TILE + (wm * 128 + r32) * GKB);
     const uint32_t sw_b = static_cast<uint32_t>(2 * TILE + wn * 2048 + r32 * 16);
     const uint32_t sw_a = static_cast<uint32_t>(2 * TILE + STILE + wm * 2048 + r32 * 16);
-    auto read_raw = [&](const uint8_t* gb, auto s_c, Raw& R) {
-        constexpr int S = decltype(s_c)::value;
+    // One of the 10 LDS reads of a stage's raw operands: weight tiles 0..3, activation
+    // tiles 4..7, scale words 8, 9.
+    auto read_part = [&](const uint8_t* gb, auto s_c, auto i_c, Raw& R) {
+        constexpr int S = decltype(s_c)::value, I = decltype(i_c)::value;
         const uint32_t chunk = static_cast<uint32_t>(((2 * S + half) ^ x7) << 4);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            R.b[t] = *reinterpret_cast<const v4u*>(gb + frow_b + t * 32 * GKB + chunk);
-            R.a[t] = *reinterpret_cast<const v4u*>(gb + frow_a + t * 32 * GKB + chunk);
-        }
-        R.wb = *reinterpret_cast<const v4u*>(gb + sw_b + S * 512);
-        R.wa = *reinterpret_cast<const v4u*>(gb + sw_a + S * 512);
+        if constexpr (I < 4) R.b[I] = *reinterpret_cast<const v4u*>(gb + frow_b + I * 32 * GKB + chunk);
+        else if constexpr (I < 8) R.a[I - 4] = *reinterpret_cast<const v4u*>(gb + frow_a + (I - 4) * 32 * GKB + chunk);
+        else if constexpr (I == 8) R.wb = *reinterpret_cast<const v4u*>(gb + sw_b + S * 512);
+        else R.wa = *reinterpret_cast<const v4u*>(gb + sw_a + S * 512);
     };
     const int sh = 16 * half;
-    // decode substep kk of R into D: dword kk of each tile, block 2h + kk/2
-    auto decode = [&](const Raw& R, auto kk_c, Dec& D) {
-        constexpr int KK = decltype(kk_c)::value;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const v2h pb = scale_pair(R.wb[t], sh);
-            const v2h pa = scale_pair(R.wa[t], sh);
-            const v2h sbt = KK < 2 ? v2h{pb[0], pb[0]} : v2h{pb[1], pb[1]};
-            const v2h sat = KK < 2 ? v2h{pa[0], pa[0]} : v2h{pa[1], pa[1]};
-            D.b[t] = decode8(R.b[t][KK], sbt);
-            D.a[t] = decode8(R.a[t][KK], sat);
-        }
+    // Part P (0..15) of decoding substep KK of R into D (dword KK of each tile, block
+    // 2h + KK/2): half P & 1 of weight tile P / 2 (P < 8) or of activation tile P / 2 - 4,
+    // i.e. two converts and two scale multiplies.
+    auto decode_part = [&](const Raw& R, auto kk_c, auto p_c, Dec& D) {
+        constexpr int KK = decltype(kk_c)::value, P = decltype(p_c)::value;
+        constexpr int t = (P >> 1) & 3, h = P & 1;
+        constexpr bool A = P >= 8;
+        const v2h pr = scale_pair(A ? R.wa[t] : R.wb[t], sh);
+        const v2h sc = KK < 2 ? v2h{pr[0], pr[0]} : v2h{pr[1], pr[1]};
+        const uint32_t w = A ? R.a[t][KK] : R.b[t][KK];
+        const v2h e0 = decode2<2 * h>(w, sc);
+        const v2h e1 = decode2<2 * h + 1>(w, sc);
+        v8h& d = A ? D.a[t] : D.b[t];
+        d[4 * h] = e0[0];
+        d[4 * h + 1] = e0[1];
+        d[4 * h + 2] = e1[0];
+        d[4 * h + 3] = e1[1];
     };
-    auto mfma16 = [&](const Dec& D) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(D.b[i], D.a[j], acc[i][j], 0, 0, 0);
+    // The 16 MFMAs of one substep on Dc, each in a slot of its own with 1/16 of the decode
+    // of (Rd, KKd) into Dn and, per the flags, one LDS read of the next stage and one load
+    // of the group after next; the slots keep the decode's VALU work spread between the
+    // MFMAs (the compiler would otherwise cluster it).
+    auto substep = [&](const Dec& Dc, const Raw& Rd, auto kkd_c, Dec& Dn, auto rd_c, const uint8_t* nb, auto sn_c,
+                       Raw& Rn, auto ld_c, auto lg_c, int lg) {
+        constexpr int RD = decltype(rd_c)::value, LD = decltype(ld_c)::value;
+        for_each_index([&](auto i_c) {
+            constexpr int i = decltype(i_c)::value;
+            acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Dc.b[i >> 2], Dc.a[i & 3], acc[i >> 2][i & 3],
+                                                                        0, 0, 0);
+            decode_part(Rd, kkd_c, i_c, Dn);
+            if constexpr (RD && i < 10) read_part(nb, sn_c, i_c, Rn);
+            if constexpr (LD == 1) issue_part(lg_c, lg, i_c);
+            if constexpr (LD == 2 && i < 2) issue_part(lg_c, lg, std::integral_constant<int, 16 + i>{});
+            __builtin_amdgcn_sched_barrier(0);
+        }, std::make_integer_sequence<int, 16>{});
     };
     Raw R0, R1;
     Dec D0, D1;
@@ -283,27 +327,23 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
         constexpr int G = decltype(g_c)::value, S = decltype(s_c)::value;
         using GN = std::integral_constant<int, (S == GS - 1) ? (G ^ 1) : G>;
         using SN = std::integral_constant<int, (S + 1) % GS>;
-        if constexpr (S == GS - 1) {
-            group_barrier<waitcnt_vm_lgkm0(0)>();
-            issue_group(g_c, g + 2);
-        }
-        decode(R, K1{}, D1);
-        mfma16(D0);
-        read_raw(gbuf(GN{}), SN{}, Rn);
-        decode(R, K2{}, D0);
-        mfma16(D1);
-        decode(R, K3{}, D1);
-        mfma16(D0);
-        decode(Rn, K0{}, D0);
-        mfma16(D1);
+        using T = std::integral_constant<int, 1>;
+        using F = std::integral_constant<int, 0>;
+        using L1 = std::integral_constant<int, (S == GS - 1) ? 1 : 0>;
+        using L2 = std::integral_constant<int, (S == GS - 1) ? 2 : 0>;
+        if constexpr (S == GS - 1) group_barrier<waitcnt_vm_lgkm0(0)>();
+        substep(D0, R, K1{}, D1, T{}, gbuf(GN{}), SN{}, Rn, L1{}, g_c, g + 2);
+        substep(D1, R, K2{}, D0, F{}, gbuf(GN{}), SN{}, Rn, L2{}, g_c, g + 2);
+        substep(D0, R, K3{}, D1, F{}, gbuf(GN{}), SN{}, Rn, F{}, g_c, g + 2);
+        substep(D1, Rn, K0{}, D0, F{}, gbuf(GN{}), SN{}, Rn, F{}, g_c, g + 2);
     };
 
     // prologue: groups 0 and 1 in flight, group 0 resident, stage 0 read and decoded
     issue_group(G0{}, 0);
     issue_group(G1{}, 1);
     group_barrier<waitcnt_vm_lgkm0(LOADS_PER_GROUP)>();
-    read_raw(lds0, S0{}, R0);
-    decode(R0, K0{}, D0);
+    for_each_index([&](auto i_c) { read_part(lds0, S0{}, i_c, R0); }, std::make_integer_sequence<int, 10>{});
+    for_each_index([&](auto p_c) { decode_part(R0, K0{}, p_c, D0); }, std::make_integer_sequence<int, 16>{});
 
     // groups in pairs (buffer = group % 2); groups past K are all zeros
     for (int g = 0; g < NG; g += 2) {

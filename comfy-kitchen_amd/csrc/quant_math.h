@@ -219,14 +219,18 @@ __device__ __forceinline__ float nvfp4_c_steps(float amax, float g, float yg) {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
-// 4 bytes of E2M1 codes -> 8 fp16 (low nibble first), times the block scale pair s.
+// Byte SEL of w (two E2M1 codes) -> 2 fp16 (low nibble first), times the scale pair s.
 // Exact: E2M1 x E4M3 products have at most 6 significant bits and lie in [2^-10, 2688]
-// (or are zero), all fp16 normals.
+// (or are zero), all fp16 normals.  (The convert's own scale operand cannot carry the
+// E4M3 scale: the hardware uses only its exponent.)
+template <int SEL>
+__device__ __forceinline__ v2h decode2(uint32_t w, v2h s) {
+    return __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, SEL) * s;
+}
+
+// 4 bytes of E2M1 codes -> 8 fp16 (low nibble first), times the block scale pair s.
 __device__ __forceinline__ v8h decode8(uint32_t w, v2h s) {
-    const v2h e0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s;
-    const v2h e1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s;
-    const v2h e2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s;
-    const v2h e3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s;
+    const v2h e0 = decode2<0>(w, s), e1 = decode2<1>(w, s), e2 = decode2<2>(w, s), e3 = decode2<3>(w, s);
     return v8h{e0[0], e0[1], e1[0], e1[1], e2[0], e2[1], e3[0], e3[1]};
 }
 
