@@ -140,8 +140,12 @@ def _sets_for(bytes_per_set: int) -> int:
 SETTLE_S = 0.3
 
 
-def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> float:
-    """Average ms per call: `make_call(i)` returns a zero-arg launcher for buffer set i.
+REPLAY_ROUNDS = 5
+
+
+def capture_graph(make_call, n_sets: int, steps: int, warmup: int, check=None):
+    """(graph, stream) of `steps` calls, `make_call(i)` returning a zero-arg launcher for
+    buffer set i; the first replay is checked with `check(outputs)`.
 
     Before the W warmup calls the op runs for SETTLE_S seconds so the GPU leaves its
     idle clock state (an MI355X ramps its clock over tens of milliseconds; timing a
@@ -162,20 +166,51 @@ def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> f
         calls[0]()  # warm the capture stream's allocator pool
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=stream):
-            outs = [calls[i % n_sets]() for i in range(steps)]
+            # Only the last n_sets outputs stay referenced, so the graph's pool hands the
+            # older output buffers to later calls, as the caching allocator does for eager
+            # calls: outputs rotate over n_sets + 1 buffers like the inputs (and like the
+            # copy floor's destinations) instead of K fresh ones.
+            outs = []
+            for i in range(steps):
+                outs.append(calls[i % n_sets]())
+                if len(outs) > n_sets:
+                    outs.pop(0)
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
     if check is not None:
         check(outs)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
+    return graph, stream
+
+
+def time_replays(graphs, steps: int, rounds: int = REPLAY_ROUNDS) -> list[float]:
+    """ms per call of each captured graph: after SETTLE_S of replays of all of them, `rounds`
+    timed replays of each, in alternating order (ABBA), each one replay of K calls between
+    HIP events on the graph's stream; the median replay is reported.  Graphs compared with
+    each other (an op and its copy floor) thus run under the same clock and memory state."""
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for g, _ in graphs:
+            g.replay()
         torch.cuda.synchronize()
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    res = [[] for _ in graphs]
+    for r in range(rounds):
+        order = range(len(graphs)) if r % 2 == 0 else reversed(range(len(graphs)))
+        for j in order:
+            graph, stream = graphs[j]
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                start.record(stream)
+                graph.replay()
+                end.record(stream)
+            torch.cuda.synchronize()
+            res[j].append(start.elapsed_time(end) / steps)
+    return [sorted(x)[len(x) // 2] for x in res]
+
+
+def time_graph(make_call, n_sets: int, steps: int, warmup: int, check=None) -> float:
+    """Median ms per call of a graph of `steps` calls (capture_graph, time_replays)."""
+    return time_replays([capture_graph(make_call, n_sets, steps, warmup, check)], steps)[0]
 
 
 def time_cpu(fn, min_reps=3, budget_s=3.0) -> tuple[float, int]:
@@ -211,9 +246,9 @@ def bench_lib():
     return _bench_lib
 
 
-def copy_floor_ms(read_bytes: int, write_bytes: int, steps: int, warmup: int) -> float:
-    """Per-call time of a streaming copy that reads and writes the given bytes, timed like the
-    ops: a HIP graph of `steps` calls over buffer sets rotating through > 512 MB."""
+def copy_floor_calls(read_bytes: int, write_bytes: int):
+    """(make_call, n_sets) of a streaming copy that reads and writes the given bytes, over
+    buffer sets rotating through > 512 MB like the ops' (benchlib/copy_floor.hip)."""
     lib = bench_lib()
     dev = torch.device("cuda", 0)
     nset = _sets_for(read_bytes + write_bytes)
@@ -228,14 +263,20 @@ def copy_floor_ms(read_bytes: int, write_bytes: int, steps: int, warmup: int) ->
             return dsts[i]
         return call
 
-    ms = time_graph(make, nset, steps, warmup)
-    del srcs, dsts
-    return ms
+    return make, nset
 
 
-def add_copy_floor(res: dict, name: str, steps: int, warmup: int, log) -> None:
-    r, w = READ_WRITE[name]
-    floor = copy_floor_ms(r, w, steps, warmup)
+def time_with_floor(name: str, make_call, n_sets: int, steps: int, warmup: int, check=None) -> tuple[float, float]:
+    """(ms per call of the op, ms per call of the copy floor for its bytes): both graphs
+    captured, then timed in alternating rounds (time_replays)."""
+    g_op = capture_graph(make_call, n_sets, steps, warmup, check)
+    fmake, fn = copy_floor_calls(*READ_WRITE[name])
+    g_floor = capture_graph(fmake, fn, steps, warmup)
+    ms, floor = time_replays([g_op, g_floor], steps)
+    return ms, floor
+
+
+def record_floor(res: dict, name: str, floor: float, log) -> None:
     res[name]["copy_floor_ms"] = floor
     res[name]["of_copy_floor"] = round(floor / res[name]["ms"], 4)
     log(f"   copy floor for {name}'s bytes: {floor * 1e3:.2f} us ({res[name]['of_copy_floor'] * 100:.1f}% of it)")
@@ -283,20 +324,20 @@ def run_gpu(configs, steps, warmup, log):
         nset = _sets_for(BYTES["quantize_per_tensor_fp8"])
         xs = [x.clone() for _ in range(nset)]
         ref_q = ck.quantize_per_tensor_fp8(x, scale)
-        ms = time_graph(lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps, warmup,
+        ms, floor = time_with_floor("quantize_per_tensor_fp8", lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps, warmup,
                         check=lambda outs: [same(o, ref_q) or sys.exit("graph replay mismatch c1 q") for o in outs])
         res["quantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_per_tensor_fp8"], ms,
                                                                       traffic.get("quantize_per_tensor_fp8"))}
         log(f"c1 quantize_per_tensor_fp8: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "quantize_per_tensor_fp8", steps, warmup, log)
+        record_floor(res, "quantize_per_tensor_fp8", floor, log)
         qs = [ref_q.clone() for _ in range(nset)]
         ref_dq = ck.dequantize_per_tensor_fp8(ref_q, scale)
-        ms = time_graph(lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
+        ms, floor = time_with_floor("dequantize_per_tensor_fp8", lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
                         check=lambda outs: [same(o, ref_dq) or sys.exit("graph replay mismatch c1 dq") for o in outs])
         res["dequantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_per_tensor_fp8"], ms,
                                                                         traffic.get("dequantize_per_tensor_fp8"))}
         log(f"c1 dequantize_per_tensor_fp8: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "dequantize_per_tensor_fp8", steps, warmup, log)
+        record_floor(res, "dequantize_per_tensor_fp8", floor, log)
         del xs, qs
 
     if "c2" in configs:
@@ -305,17 +346,17 @@ def run_gpu(configs, steps, warmup, log):
         qs = [q.clone() for _ in range(nset)]
         ks = [k.clone() for _ in range(nset)]
         rq, rk = ck.apply_rope(q, k, f)
-        ms = time_graph(lambda i: (lambda: ck.apply_rope(qs[i], ks[i], f)), nset, steps, warmup,
+        ms, floor = time_with_floor("apply_rope", lambda i: (lambda: ck.apply_rope(qs[i], ks[i], f)), nset, steps, warmup,
                         check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
         res["apply_rope"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope"], ms, traffic.get("apply_rope"))}
         log(f"c2 apply_rope: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "apply_rope", steps, warmup, log)
+        record_floor(res, "apply_rope", floor, log)
         rq1 = ck.apply_rope1(q, f)
-        ms = time_graph(lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
+        ms, floor = time_with_floor("apply_rope1", lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
                         check=lambda outs: [same(o, rq1) or sys.exit("graph mismatch c2 rope1") for o in outs])
         res["apply_rope1"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope1"], ms, traffic.get("apply_rope1"))}
         log(f"c2 apply_rope1: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "apply_rope1", steps, warmup, log)
+        record_floor(res, "apply_rope1", floor, log)
         del qs, ks
 
     if "c3" in configs or "c4" in configs:
@@ -324,25 +365,25 @@ def run_gpu(configs, steps, warmup, log):
         if "c3" in configs:
             nset = _sets_for(BYTES["quantize_mxfp8"])
             xs = [x.clone() for _ in range(nset)]
-            ms = time_graph(lambda i: (lambda: ck.quantize_mxfp8(xs[i])), nset, steps, warmup,
+            ms, floor = time_with_floor("quantize_mxfp8", lambda i: (lambda: ck.quantize_mxfp8(xs[i])), nset, steps, warmup,
                             check=lambda outs: [(same(a, qa) and same(b, sa)) or sys.exit("graph mismatch c3")
                                                 for a, b in outs])
             res["quantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_mxfp8"], ms,
                                                                  traffic.get("quantize_mxfp8"))}
             log(f"c3 quantize_mxfp8: {ms * 1e3:.2f} us")
-            add_copy_floor(res, "quantize_mxfp8", steps, warmup, log)
+            record_floor(res, "quantize_mxfp8", floor, log)
             del xs
             # the layouts' dequantize of the same tensor (bf16 out)
             want = ck.dequantize_mxfp8(qa, sa)
             nset = _sets_for(BYTES["dequantize_mxfp8"])
             qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
-            ms = time_graph(lambda i: (lambda: ck.dequantize_mxfp8(*qs_[i])), nset, steps, warmup,
+            ms, floor = time_with_floor("dequantize_mxfp8", lambda i: (lambda: ck.dequantize_mxfp8(*qs_[i])), nset, steps, warmup,
                             check=lambda outs: [same(o, want) or sys.exit("graph mismatch c3 dequantize")
                                                 for o in outs])
             res["dequantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_mxfp8"], ms,
                                                                    traffic.get("dequantize_mxfp8"))}
             log(f"c3 dequantize_mxfp8: {ms * 1e3:.2f} us")
-            add_copy_floor(res, "dequantize_mxfp8", steps, warmup, log)
+            record_floor(res, "dequantize_mxfp8", floor, log)
             del qs_, want
         if "c4" in configs:
             qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
@@ -382,12 +423,12 @@ def run_gpu(configs, steps, warmup, log):
         qa, sa = ck.quantize_nvfp4(a, ga)
         nset = _sets_for(BYTES["quantize_nvfp4"])
         as_ = [a.clone() for _ in range(nset)]
-        ms = time_graph(lambda i: (lambda: ck.quantize_nvfp4(as_[i], ga)), nset, steps, warmup,
-                        check=lambda outs: [(same(x_, qa) and same(y_, sa)) or sys.exit("graph mismatch c5")
-                                            for x_, y_ in outs])
+        ms, floor = time_with_floor("quantize_nvfp4", lambda i: (lambda: ck.quantize_nvfp4(as_[i], ga)), nset, steps,
+                                    warmup, check=lambda outs: [(same(x_, qa) and same(y_, sa))
+                                                                or sys.exit("graph mismatch c5") for x_, y_ in outs])
         res["quantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["quantize_nvfp4"], ms, traffic.get("quantize_nvfp4"))}
         log(f"c5 quantize_nvfp4: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "quantize_nvfp4", steps, warmup, log)
+        record_floor(res, "quantize_nvfp4", floor, log)
         # dynamic scale (the layouts' scale=None): the fused call against amax_scale + quantize
         g_dyn = ck.amax_scale(a, 2688.0)
         q_dyn, s_dyn = ck.quantize_nvfp4(a, g_dyn)
@@ -411,12 +452,12 @@ def run_gpu(configs, steps, warmup, log):
         want = ck.dequantize_nvfp4(qa, ga, sa)
         nset = _sets_for(BYTES["dequantize_nvfp4"])
         qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
-        ms = time_graph(lambda i: (lambda: ck.dequantize_nvfp4(qs_[i][0], ga, qs_[i][1])), nset, steps, warmup,
+        ms, floor = time_with_floor("dequantize_nvfp4", lambda i: (lambda: ck.dequantize_nvfp4(qs_[i][0], ga, qs_[i][1])), nset, steps, warmup,
                         check=lambda outs: [same(o, want) or sys.exit("graph mismatch c5 dequantize") for o in outs])
         res["dequantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_nvfp4"], ms,
                                                                traffic.get("dequantize_nvfp4"))}
         log(f"c5 dequantize_nvfp4: {ms * 1e3:.2f} us")
-        add_copy_floor(res, "dequantize_nvfp4", steps, warmup, log)
+        record_floor(res, "dequantize_nvfp4", floor, log)
         del qs_, want
         qw, sw = ck.quantize_nvfp4(w, gw)
         try:
