@@ -744,6 +744,101 @@ def summarize_counters(sq_dir: str, configs, command: str):
                   f"{ratio} |")
 
 
+# (config, kernel-name substring of the op's timed kernel, algorithmic units) per op, for the
+# per-op profile summaries
+PROFILE_OPS = {
+    "quantize_per_tensor_fp8": ("c1", "quantize_fp8_kernel<2, 5, true>"),
+    "dequantize_per_tensor_fp8": ("c1", "dequantize_fp8_kernel<5, 2, true>"),
+    "apply_rope": ("c2", "rope_wave_kernel<2, 0, false>"),
+    "apply_rope1": ("c2", "rope_wave_kernel<2, 0, true>"),
+    "quantize_mxfp8": ("c3", "quantize_mxfp8_fast_kernel<2>"),
+    "dequantize_mxfp8": ("c3", "dequantize_mxfp8_fast_kernel<2>"),
+    "scaled_mm_mxfp8": ("c4", "mx::gemm_kernel<2, -1, false, -1>"),
+    "quantize_nvfp4": ("c5", "quantize_nvfp4_fast_kernel<2, true, 16, false>"),
+    "dequantize_nvfp4": ("c5", "dequantize_nvfp4_tile_kernel<2, true>"),
+    "scaled_mm_nvfp4": ("c5", "nv::gemm_kernel<2, -1>"),
+}
+
+
+def summarize_trace(kt_dir: str, bench_json: str, command: str):
+    """profiles/<op>_<config>.md from a rocprofv3 --kernel-trace run of bench.py (graph-replay
+    dispatches: runs of >= 20 back-to-back dispatches of the op's kernel), the bench line of
+    a run without the profiler, profiles/traffic.json and profiles/counters.json."""
+    import csv
+    import statistics
+
+    rows = []
+    for f in sorted(Path(kt_dir).rglob("*kernel_trace.csv")):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    line = json.loads(Path(bench_json).read_text().strip().splitlines()[-1])
+    prof = REPO / "profiles"
+    traffic = json.loads((prof / "traffic.json").read_text()) if (prof / "traffic.json").exists() else {}
+    counters = json.loads((prof / "counters.json").read_text()) if (prof / "counters.json").exists() else {}
+    for op, (cfg, sub) in PROFILE_OPS.items():
+        res = line["ops"].get(op)
+        if res is None or "ms" not in res:
+            continue
+        durs, run, name = [], [], None
+        for i, (s0, e0, k) in enumerate(rows):
+            mine = sub in k
+            if mine and run and s0 - rows[run[-1]][1] < 5000 and run[-1] == i - 1:
+                run.append(i)
+                continue
+            if len(run) >= 20:
+                durs += [(rows[j][1] - rows[j][0]) / 1e3 for j in run]
+            run = [i] if mine else []
+            if mine:
+                name = k
+        if len(run) >= 20:
+            durs += [(rows[j][1] - rows[j][0]) / 1e3 for j in run]
+        if not durs:
+            continue
+        us = res["ms"] * 1e3
+        out = [f"# {op} — BASELINE {cfg}", "",
+               "Kernel durations from the kernel trace of a bench run, over the op's HIP-graph replays (runs of",
+               "back-to-back dispatches of its kernel: the settle replays and the five timed rounds):", "",
+               f"    {command}", "",
+               "| kernel | dispatches | mean µs | median µs | min µs | max µs |", "|---|---|---|---|---|---|",
+               f"| `{name[:110]}` | {len(durs)} | {statistics.mean(durs):.2f} | {statistics.median(durs):.2f} | "
+               f"{min(durs):.2f} | {max(durs):.2f} |", "",
+               f"bench.py without the profiler (`python -u bench.py`, median of five graph replays of K calls between "
+               f"HIP events on the launch stream): **{us:.2f} µs** per call → {res['achieved']} {res['unit']} = "
+               f"{100 * res['frac']:.1f}% of {res['peak']} {res['unit']}."]
+        if "copy_floor_ms" in res:
+            out += ["", f"Copy floor for the same bytes in the same run (`benchlib/copy_floor.hip`, timed in alternating "
+                        f"rounds with the op): {res['copy_floor_ms'] * 1e3:.2f} µs; the op runs at "
+                        f"{100 * res['of_copy_floor']:.1f}% of it."]
+        t = traffic.get("bytes_per_launch", {}).get(op)
+        if t:
+            cal = traffic.get("calibration", {})
+            out += ["", "L2-miss bytes per launch, i.e. HBM traffic plus Infinity-Cache hits (rocprofv3 `--pmc "
+                        "FETCH_SIZE`, then `--pmc WRITE_SIZE`, over `python -u bench.py --pmc-driver`, three eager "
+                        "calls on the same buffers, scaled by a 256 MiB calibration kernel: FETCH "
+                        f"×{cal.get('FETCH_SIZE', {}).get('factor', '?')}, WRITE ×{cal.get('WRITE_SIZE', {}).get('factor', '?')}):",
+                    "", "| fetched B | written B | total B |", "|---|---|---|",
+                    f"| {t.get('fetch', 0):,} | {t.get('write', 0):,} | {t.get('total', 0):,} |"]
+        c = counters.get("ops", {}).get(op)
+        if c and c[0].get("valu_insts_per_mfma") is not None:
+            e = c[0]
+            out += ["", "## MFMA busy and LDS conflicts (SQ counters, one pass; `profiles/counters.json`)", "",
+                    f"    {counters.get('command', '')}", "",
+                    "MFMA busy = (SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES) of the GEMM's dispatch ÷ the same ratio of "
+                    "a calibration loop of back-to-back MFMAs on every SIMD (`benchlib/mfma_loop.hip`, "
+                    f"{counters['calibration']['mfma_busy_per_sq_busy']}), averaged over {e['dispatches']} eager calls "
+                    "on the same operands.", "",
+                    "| kernel | MFMA busy | MFMA insts | LDS insts | LDS bank-conflict cycles | per LDS inst | "
+                    "LDS address conflicts | VALU insts per MFMA |", "|---|---|---|---|---|---|---|---|",
+                    f"| `{e['kernel']}` | {100 * e['mfma_busy']:.1f}% | {e['SQ_INSTS_MFMA']:,} | {e['SQ_INSTS_LDS']:,} | "
+                    f"{e['SQ_LDS_BANK_CONFLICT']:,} | {e['lds_bank_conflict_cycles_per_lds_inst']} | "
+                    f"{e['SQ_LDS_ADDR_CONFLICT']:,} | {e['valu_insts_per_mfma']} |"]
+        (prof / f"{op}_{cfg}.md").write_text("\n".join(out) + "\n")
+        print(f"wrote profiles/{op}_{cfg}.md ({len(durs)} dispatches, mean {statistics.mean(durs):.2f} us, "
+              f"bench {us:.2f} us)")
+
+
 def pmc_sequence_names(configs):
     names = []
     if "c1" in configs:
@@ -770,14 +865,20 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc output directories")
     ap.add_argument("--pmc-command", default="", help="command recorded in profiles/traffic.json")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("KT_DIR", "BENCH_JSON"),
+                    help="write profiles/<op>_<config>.md from a rocprofv3 --kernel-trace run and a bench line")
     ap.add_argument("--summarize-counters", metavar="SQ_DIR",
                     help="write profiles/counters.json (MFMA busy, LDS conflicts) from a rocprofv3 --pmc pass "
                          "over SQ_COUNTERS")
     args = ap.parse_args()
     if args.summarize_pmc:
         summarize_pmc(*args.summarize_pmc, set(args.configs.split(",")), args.pmc_command)
+        return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters, set(args.configs.split(",")), args.pmc_command)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace, args.pmc_command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
