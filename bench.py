@@ -781,19 +781,20 @@ def summarize_trace(kt_dir: str, bench_json: str, command: str):
         res = line["ops"].get(op)
         if res is None or "ms" not in res:
             continue
-        durs, run, name = [], [], None
-        for i, (s0, e0, k) in enumerate(rows):
-            mine = sub in k
-            if mine and run and s0 - rows[run[-1]][1] < 5000 and run[-1] == i - 1:
-                run.append(i)
-                continue
-            if len(run) >= 20:
-                durs += [(rows[j][1] - rows[j][0]) / 1e3 for j in run]
-            run = [i] if mine else []
-            if mine:
-                name = k
+        # the op's dispatches, grouped into runs separated by more than 20 us (or 5% of a
+        # dispatch) of idle time: an op may launch a small kernel of its own in between
+        # (the NVFP4 GEMM's alpha product), so other kernels do not split a run
+        mine = [(s0, e0, k) for s0, e0, k in rows if sub in k]
+        durs, run = [], []
+        for d in mine:
+            if run and d[0] - run[-1][1] > max(20000, (run[-1][1] - run[-1][0]) // 20):
+                if len(run) >= 20:
+                    durs += [(e0 - s0) / 1e3 for s0, e0, _ in run]
+                run = []
+            run.append(d)
         if len(run) >= 20:
-            durs += [(rows[j][1] - rows[j][0]) / 1e3 for j in run]
+            durs += [(e0 - s0) / 1e3 for s0, e0, _ in run]
+        name = mine[0][2] if mine else ""
         if not durs:
             continue
         us = res["ms"] * 1e3
