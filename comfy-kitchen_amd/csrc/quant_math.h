@@ -126,40 +126,6 @@ __device__ __forceinline__ uint2 mx_codes16(uint4 w, uint32_t bits, uint32_t& e)
     return mx_encode8(v, bits, e);
 }
 
-// The codes of a block whose scale is 0.0 (exponent 0 with a nonzero amax: a tiny or
-// non-finite amax): x / 0 is +-inf, clamped to 0x7E | sign, for a nonzero non-NaN x, and
-// NaN, 0xFF, for x = +-0 or NaN.  Straight-line bit operations.
-template <int IN>
-__device__ __forceinline__ uint2 mx_codes16_scale0(uint4 w) {
-    constexpr uint32_t kInf = IN == CKH_BF16 ? 0x7f80u : 0x7c00u;
-    const uint32_t h[4] = {w.x, w.y, w.z, w.w};
-    uint32_t c[2] = {0u, 0u};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const uint32_t x = (h[t >> 1] >> (16 * (t & 1))) & 0xffffu, a = x & 0x7fffu;
-        const uint32_t code = (a == 0 || a > kInf) ? 0xffu : (0x7eu | ((x >> 8) & 0x80u));
-        c[t >> 2] |= code << (8 * (t & 3));
-    }
-    return make_uint2(c[0], c[1]);
-}
-
-// mx_codes16 with no float arrays or software encoders, for callers with no registers to
-// spare (the bf16-activation GEMM): the same codes and exponent for every input.  With e =
-// mx_exponent(amax) >= 1 the scale 2^(e-127) >= amax/448 is normal and the scaled convert
-// equals the reference's x / scale -> E4M3 (the MXFP8 hardware identity); e == 0 means a
-// zero block (+0 codes), or a scale of 0.0 (tiny or non-finite amax), for which x / 0
-// gives 0x7E | sign for a nonzero non-NaN x (clamped +-inf) and 0xFF for 0 or NaN.
-template <int IN>
-__device__ __forceinline__ uint2 mx_codes16_compact(uint4 w, uint32_t bits, uint32_t& e) {
-    e = mx_exponent(bits);
-    if (e != 0) {
-        const float scale = as_f(e << 23);
-        return make_uint2(scaled_e4m3x4<IN>(w.x, w.y, scale), scaled_e4m3x4<IN>(w.z, w.w, scale));
-    }
-    if (bits == 0) return make_uint2(0u, 0u);
-    return mx_codes16_scale0<IN>(w);
-}
-
 // mx_exponent without branches (the same value for every input): the closed form on the
 // common range, 0 for non-finite amax, and for amax below 2^-117 (biased exponent < 10)
 // two thresholds: the division form s = RN(amax / 448) gives e = 0 up to amax bits
