@@ -324,16 +324,18 @@ def run_gpu(configs, steps, warmup, log):
         nset = _sets_for(BYTES["quantize_per_tensor_fp8"])
         xs = [x.clone() for _ in range(nset)]
         ref_q = ck.quantize_per_tensor_fp8(x, scale)
-        ms, floor = time_with_floor("quantize_per_tensor_fp8", lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps, warmup,
-                        check=lambda outs: [same(o, ref_q) or sys.exit("graph replay mismatch c1 q") for o in outs])
+        ms, floor = time_with_floor(
+            "quantize_per_tensor_fp8", lambda i: (lambda: ck.quantize_per_tensor_fp8(xs[i], scale)), nset, steps,
+            warmup, check=lambda outs: [same(o, ref_q) or sys.exit("graph replay mismatch c1 q") for o in outs])
         res["quantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_per_tensor_fp8"], ms,
                                                                       traffic.get("quantize_per_tensor_fp8"))}
         log(f"c1 quantize_per_tensor_fp8: {ms * 1e3:.2f} us")
         record_floor(res, "quantize_per_tensor_fp8", floor, log)
         qs = [ref_q.clone() for _ in range(nset)]
         ref_dq = ck.dequantize_per_tensor_fp8(ref_q, scale)
-        ms, floor = time_with_floor("dequantize_per_tensor_fp8", lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps, warmup,
-                        check=lambda outs: [same(o, ref_dq) or sys.exit("graph replay mismatch c1 dq") for o in outs])
+        ms, floor = time_with_floor(
+            "dequantize_per_tensor_fp8", lambda i: (lambda: ck.dequantize_per_tensor_fp8(qs[i], scale)), nset, steps,
+            warmup, check=lambda outs: [same(o, ref_dq) or sys.exit("graph replay mismatch c1 dq") for o in outs])
         res["dequantize_per_tensor_fp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_per_tensor_fp8"], ms,
                                                                         traffic.get("dequantize_per_tensor_fp8"))}
         log(f"c1 dequantize_per_tensor_fp8: {ms * 1e3:.2f} us")
@@ -346,14 +348,16 @@ def run_gpu(configs, steps, warmup, log):
         qs = [q.clone() for _ in range(nset)]
         ks = [k.clone() for _ in range(nset)]
         rq, rk = ck.apply_rope(q, k, f)
-        ms, floor = time_with_floor("apply_rope", lambda i: (lambda: ck.apply_rope(qs[i], ks[i], f)), nset, steps, warmup,
-                        check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
+        ms, floor = time_with_floor(
+            "apply_rope", lambda i: (lambda: ck.apply_rope(qs[i], ks[i], f)), nset, steps, warmup,
+            check=lambda outs: [(same(a, rq) and same(b, rk)) or sys.exit("graph mismatch c2") for a, b in outs])
         res["apply_rope"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope"], ms, traffic.get("apply_rope"))}
         log(f"c2 apply_rope: {ms * 1e3:.2f} us")
         record_floor(res, "apply_rope", floor, log)
         rq1 = ck.apply_rope1(q, f)
-        ms, floor = time_with_floor("apply_rope1", lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
-                        check=lambda outs: [same(o, rq1) or sys.exit("graph mismatch c2 rope1") for o in outs])
+        ms, floor = time_with_floor(
+            "apply_rope1", lambda i: (lambda: ck.apply_rope1(qs[i], f)), nset, steps, warmup,
+            check=lambda outs: [same(o, rq1) or sys.exit("graph mismatch c2 rope1") for o in outs])
         res["apply_rope1"] = {"ms": ms, **roofline_bytes(BYTES["apply_rope1"], ms, traffic.get("apply_rope1"))}
         log(f"c2 apply_rope1: {ms * 1e3:.2f} us")
         record_floor(res, "apply_rope1", floor, log)
@@ -365,9 +369,9 @@ def run_gpu(configs, steps, warmup, log):
         if "c3" in configs:
             nset = _sets_for(BYTES["quantize_mxfp8"])
             xs = [x.clone() for _ in range(nset)]
-            ms, floor = time_with_floor("quantize_mxfp8", lambda i: (lambda: ck.quantize_mxfp8(xs[i])), nset, steps, warmup,
-                            check=lambda outs: [(same(a, qa) and same(b, sa)) or sys.exit("graph mismatch c3")
-                                                for a, b in outs])
+            ms, floor = time_with_floor(
+                "quantize_mxfp8", lambda i: (lambda: ck.quantize_mxfp8(xs[i])), nset, steps, warmup,
+                check=lambda outs: [(same(a, qa) and same(b, sa)) or sys.exit("graph mismatch c3") for a, b in outs])
             res["quantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["quantize_mxfp8"], ms,
                                                                  traffic.get("quantize_mxfp8"))}
             log(f"c3 quantize_mxfp8: {ms * 1e3:.2f} us")
@@ -377,9 +381,9 @@ def run_gpu(configs, steps, warmup, log):
             want = ck.dequantize_mxfp8(qa, sa)
             nset = _sets_for(BYTES["dequantize_mxfp8"])
             qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
-            ms, floor = time_with_floor("dequantize_mxfp8", lambda i: (lambda: ck.dequantize_mxfp8(*qs_[i])), nset, steps, warmup,
-                            check=lambda outs: [same(o, want) or sys.exit("graph mismatch c3 dequantize")
-                                                for o in outs])
+            ms, floor = time_with_floor(
+                "dequantize_mxfp8", lambda i: (lambda: ck.dequantize_mxfp8(*qs_[i])), nset, steps, warmup,
+                check=lambda outs: [same(o, want) or sys.exit("graph mismatch c3 dequantize") for o in outs])
             res["dequantize_mxfp8"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_mxfp8"], ms,
                                                                    traffic.get("dequantize_mxfp8"))}
             log(f"c3 dequantize_mxfp8: {ms * 1e3:.2f} us")
@@ -423,9 +427,9 @@ def run_gpu(configs, steps, warmup, log):
         qa, sa = ck.quantize_nvfp4(a, ga)
         nset = _sets_for(BYTES["quantize_nvfp4"])
         as_ = [a.clone() for _ in range(nset)]
-        ms, floor = time_with_floor("quantize_nvfp4", lambda i: (lambda: ck.quantize_nvfp4(as_[i], ga)), nset, steps,
-                                    warmup, check=lambda outs: [(same(x_, qa) and same(y_, sa))
-                                                                or sys.exit("graph mismatch c5") for x_, y_ in outs])
+        ms, floor = time_with_floor(
+            "quantize_nvfp4", lambda i: (lambda: ck.quantize_nvfp4(as_[i], ga)), nset, steps, warmup,
+            check=lambda outs: [(same(x_, qa) and same(y_, sa)) or sys.exit("graph mismatch c5") for x_, y_ in outs])
         res["quantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["quantize_nvfp4"], ms, traffic.get("quantize_nvfp4"))}
         log(f"c5 quantize_nvfp4: {ms * 1e3:.2f} us")
         record_floor(res, "quantize_nvfp4", floor, log)
@@ -452,8 +456,9 @@ def run_gpu(configs, steps, warmup, log):
         want = ck.dequantize_nvfp4(qa, ga, sa)
         nset = _sets_for(BYTES["dequantize_nvfp4"])
         qs_ = [(qa.clone(), sa.clone()) for _ in range(nset)]
-        ms, floor = time_with_floor("dequantize_nvfp4", lambda i: (lambda: ck.dequantize_nvfp4(qs_[i][0], ga, qs_[i][1])), nset, steps, warmup,
-                        check=lambda outs: [same(o, want) or sys.exit("graph mismatch c5 dequantize") for o in outs])
+        ms, floor = time_with_floor(
+            "dequantize_nvfp4", lambda i: (lambda: ck.dequantize_nvfp4(qs_[i][0], ga, qs_[i][1])), nset, steps,
+            warmup, check=lambda outs: [same(o, want) or sys.exit("graph mismatch c5 dequantize") for o in outs])
         res["dequantize_nvfp4"] = {"ms": ms, **roofline_bytes(BYTES["dequantize_nvfp4"], ms,
                                                                traffic.get("dequantize_nvfp4"))}
         log(f"c5 dequantize_nvfp4: {ms * 1e3:.2f} us")
