@@ -752,7 +752,7 @@ def summarize_counters(sq_dir: str, configs, command: str):
 # (config, kernel-name substring of the op's timed kernel, algorithmic units) per op, for the
 # per-op profile summaries
 PROFILE_OPS = {
-    "quantize_per_tensor_fp8": ("c1", "quantize_fp8_kernel<2, 5, true>"),
+    "quantize_per_tensor_fp8": ("c1", "quantize_fp8_pipe_kernel<2, 5>"),
     "dequantize_per_tensor_fp8": ("c1", "dequantize_fp8_kernel<5, 2, true>"),
     "apply_rope": ("c2", "rope_wave_kernel<2, 0, false>"),
     "apply_rope1": ("c2", "rope_wave_kernel<2, 0, true>"),

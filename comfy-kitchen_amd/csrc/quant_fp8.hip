@@ -8,9 +8,10 @@
 // For bf16/f16 inputs the product of two 16-bit floats is exact in fp32, so rounding
 // the fp32 product to the 16-bit type equals the 16-bit multiply of the reference.
 //
-// Launch shape: 256 threads, 16 elements per thread (one 16-byte FP8 store; two
-// 16-byte loads for 16-bit inputs), one tile per thread, no grid-stride loop: the
-// configs have >= 3k workgroups, enough to fill 256 CUs several times over.
+// Launch shape: aligned 16-bit inputs of at least 1024 elements take a persistent kernel
+// whose waves walk 1024-element tiles with the next tile's loads in flight
+// (quantize_fp8_pipe_kernel); other quantize calls and every dequantize use 128-thread
+// workgroups with 16 elements per thread, one tile per thread.
 #include "ckh_common.h"
 
 namespace ckh {
@@ -84,6 +85,101 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
         for (int64_t i = ib; i < n && i < ib + 8; ++i)
             out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
     }
+}
+
+// One wave-tile (1024 elements; lane l: pieces l and 64 + l) of the quantizer from its
+// raw loads: codes stored, a NaN-containing lane re-encoded by the software path.
+template <int IN, int OUT>
+__device__ __forceinline__ void quantize_tile(const Raw8<IN>& ra, const Raw8<IN>& rb, float r, uint8_t* out,
+                                              int64_t ia, int64_t ib) {
+    float v[16];
+    unpack8<IN>(ra, *reinterpret_cast<float(*)[8]>(&v[0]));
+    unpack8<IN>(rb, *reinterpret_cast<float(*)[8]>(&v[8]));
+    float t[16];
+    bool any_nan = false;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        t[e] = round_to_hw<IN>(v[e] * r);
+        any_nan |= is_nan(t[e]);
+    }
+    constexpr float MX = OUT == CKH_E4M3 ? 448.0f : 57344.0f;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float c[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) c[b] = __builtin_amdgcn_fmed3f(t[4 * q + b], -MX, MX);
+        w[q] = OUT == CKH_E4M3 ? hw_e4m3x4(c[0], c[1], c[2], c[3]) : hw_e5m2x4(c[0], c[1], c[2], c[3]);
+    }
+    if (any_nan) {  // keep the software's NaN bytes
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
+            w[q] = acc;
+        }
+    }
+    st_stream8(out + ia, make_uint2(w[0], w[1]));
+    st_stream8(out + ib, make_uint2(w[2], w[3]));
+}
+
+// Persistent form for aligned 16-bit inputs: the grid's W waves (about kQWavesPerCU per CU,
+// with the whole wave-tiles spread evenly over them) each walk tiles t = w, w + W, ...,
+// issuing the loads of tile t + W before converting and storing tile t, so every wave
+// keeps a tile in flight while it computes.  Elements past the last whole tile are done
+// by wave 0 with the scalar path.  Same-process A/B on C1 against the one-tile-per-lane
+// kernel below: 93.2% vs 90.8% and 91.7% vs 89.6% of the copy floor (16 waves per CU;
+// 8, 12, 24 and 32 measured 87-90%).
+constexpr int kQWavesPerCU = 16;
+
+template <int IN, int OUT>
+__global__ __launch_bounds__(256) void quantize_fp8_pipe_kernel(const void* __restrict__ x,
+                                                                const float* __restrict__ scale,
+                                                                uint8_t* __restrict__ out, int64_t n) {
+    constexpr int ES = ElemSize<IN>::value;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t W = gridDim.x * 4u;
+    const uint32_t w0 = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t tiles = static_cast<uint32_t>(n >> 10);
+    const char* xb = static_cast<const char*>(x);
+    uint32_t t = w0;
+    Raw8<IN> ra{}, rb{};
+    if (t < tiles) {
+        ra = load8_raw<IN>(xb + (static_cast<int64_t>(t) * 1024 + 8 * lane) * ES);
+        rb = load8_raw<IN>(xb + (static_cast<int64_t>(t) * 1024 + 512 + 8 * lane) * ES);
+    }
+    const float r = round_to<IN>(1.0f / scale[0]);
+    while (t < tiles) {
+        const uint32_t tn = t + W;
+        Raw8<IN> na = ra, nb = rb;
+        if (tn < tiles) {
+            na = load8_raw<IN>(xb + (static_cast<int64_t>(tn) * 1024 + 8 * lane) * ES);
+            nb = load8_raw<IN>(xb + (static_cast<int64_t>(tn) * 1024 + 512 + 8 * lane) * ES);
+        }
+        const int64_t ia = static_cast<int64_t>(t) * 1024 + 8 * lane;
+        quantize_tile<IN, OUT>(ra, rb, r, out, ia, ia + 512);
+        t = tn;
+        ra = na;
+        rb = nb;
+    }
+    if (w0 == 0) {
+        for (int64_t i = static_cast<int64_t>(tiles) * 1024 + lane; i < n; i += 64)
+            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+    }
+}
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
 }
 
 template <int IN>
@@ -203,6 +299,26 @@ extern "C" int ckh_quantize_fp8(const void* x, const void* scale, void* out, int
     CKH_REQUIRE(out_code == CKH_E4M3 || out_code == CKH_E5M2, "quantize_fp8: unsupported output dtype code %d",
                 out_code);
     const bool vec = aligned(x, 16) && aligned(out, 16);
+    if (vec && in_code != CKH_F32 && numel >= 1024) {
+        // waves: at most kQWavesPerCU per CU, as many tiles per wave as that forces, and the
+        // tiles spread evenly over the waves
+        const int64_t tiles = numel >> 10;
+        const int64_t per_wave = cdiv(tiles, static_cast<int64_t>(device_cus()) * kQWavesPerCU);
+        const dim3 pgrid(static_cast<unsigned>(cdiv(cdiv(tiles, per_wave), 4)));
+        hipStream_t pst = reinterpret_cast<hipStream_t>(stream);
+        const float* psp = static_cast<const float*>(scale);
+        uint8_t* po = static_cast<uint8_t*>(out);
+#define LAUNCH_P(I, O) hipLaunchKernelGGL((quantize_fp8_pipe_kernel<I, O>), pgrid, dim3(256), 0, pst, x, psp, po, numel)
+        if (out_code == CKH_E4M3) {
+            if (in_code == CKH_F16) LAUNCH_P(CKH_F16, CKH_E4M3);
+            else LAUNCH_P(CKH_BF16, CKH_E4M3);
+        } else {
+            if (in_code == CKH_F16) LAUNCH_P(CKH_F16, CKH_E5M2);
+            else LAUNCH_P(CKH_BF16, CKH_E5M2);
+        }
+#undef LAUNCH_P
+        return check_launch("quantize_fp8");
+    }
     dim3 grid(static_cast<unsigned>(cdiv(numel, kThreads * kPerThread)));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float* sp = static_cast<const float*>(scale);
