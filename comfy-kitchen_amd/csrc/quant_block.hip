@@ -271,8 +271,10 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 
 // ------------------------------------------------------- NVFP4, 16-bit fast path
 // For bf16/f16 inputs with no column padding, cols % 64 == 0, 16-byte aligned, < 2^31
-// elements.  One lane per 16-element block (two 16-byte streaming loads), four lanes
-// per unit (one scale word), two units per thread.  The IEEE divisions of the
+// elements.  One lane per 16-element block, four lanes per unit (one scale word), two
+// units per thread.  A lane's block is two 16-byte chunks that another lane's loads
+// share (nv_pair_exchange), so that each load instruction reads one contiguous KB
+// rather than every other 16 bytes of 2 KB (which measured 6% slower).  The IEEE divisions of the
 // reference are replaced by Markstein correction steps, each exact:
 //   c = (amax / 6) / g:  c0 = amax*y6, c1 = fma(-fma(6, c0, -amax), y6, c0), then the
 //                        same step with y_g = RN(1/g) (one IEEE division per thread);
@@ -303,6 +305,25 @@ __device__ __forceinline__ uint2 nvfp4_codes16_exact(const float (&v)[16], float
 #pragma unroll
     for (int t = 0; t < 16; ++t) q[t] = markstein_quotient(v[t], T, y);
     return make_uint2(pack_e2m1x8<HI_FIRST>(&q[0]), pack_e2m1x8<HI_FIRST>(&q[8]));
+}
+
+// Lanes t and t + 4 of a wave (bit 2 of t clear: "low", set: "high") load the two 16-byte
+// halves of a pair of blocks A and B: the low lane the first halves (P = A0, Q = B0), the
+// high lane the second (P = A1, Q = B1).  After the exchange the low lane holds block A
+// (A0, A1) and the high lane block B (B0, B1).  DPP rows are 16 lanes; bank_mask selects
+// the 4-lane banks written (0x5: banks 0, 2 = low lanes; 0xA: banks 1, 3 = high lanes).
+__device__ __forceinline__ void nv_pair_exchange(uint4& P, uint4& Q) {
+    auto lo_half = [](uint32_t p, uint32_t q) {  // high lanes: q of lane t - 4 (row_shr:4)
+        return static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(static_cast<int>(p), static_cast<int>(q), 0x114, 0xf, 0xa, false));
+    };
+    auto hi_half = [](uint32_t q, uint32_t p) {  // low lanes: p of lane t + 4 (row_shl:4)
+        return static_cast<uint32_t>(
+            __builtin_amdgcn_update_dpp(static_cast<int>(q), static_cast<int>(p), 0x104, 0xf, 0x5, false));
+    };
+    const uint4 a = P, b = Q;
+    P = make_uint4(lo_half(a.x, b.x), lo_half(a.y, b.y), lo_half(a.z, b.z), lo_half(a.w, b.w));
+    Q = make_uint4(hi_half(b.x, a.x), hi_half(b.y, a.y), hi_half(b.z, a.z), hi_half(b.w, a.w));
 }
 
 constexpr int kNvUnits = 2;  // units per thread: 2 passes cover a workgroup's 32 rows x G units
@@ -338,15 +359,27 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
-        ul[u] = u * kUnitsPerPass + (threadIdx.x >> 2);  // unit in the workgroup
-        const uint32_t rs = ul[u] / G;                   // row slot: 8 rows x 4 groups
-        r[u] = it.tile * 128 + (rs & 3) * 32 + it.q * 8 + (rs >> 2);
-        j[u] = it.cg * G + ul[u] % G;
+        // The wave's 16 units (2 KB): A block k is block k of its first KB, B block k of
+        // its second, and lanes t, t + 4 with k = 4 (t / 8) + t % 4 share them
+        // (nv_pair_exchange).  Each load instruction then reads one contiguous KB.
+        const uint32_t t = threadIdx.x & 63, hi = (t >> 2) & 1, k = 4 * (t >> 3) + (t & 3);
+        const uint32_t wb = u * kUnitsPerPass + (threadIdx.x >> 6) * 16;
+        ul[u] = wb + 8 * hi + (t >> 3);  // unit in the workgroup of the lane's own block
+        uint32_t rr[2], jj[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t uu = wb + 8 * h + (k >> 2);  // unit of A (h = 0) / B (h = 1) block k
+            const uint32_t rs = uu / G;                 // row slot: 8 rows x 4 groups
+            rr[h] = it.tile * 128 + (rs & 3) * 32 + it.q * 8 + (rs >> 2);
+            jj[h] = it.cg * G + uu % G;
+        }
+        r[u] = rr[hi];
+        j[u] = jj[hi];
         off[u] = r[u] * cols + 64 * j[u] + 16 * l;
-        w[u][0] = w[u][1] = make_uint4(0u, 0u, 0u, 0u);
-        if (r[u] < rows && j[u] < n_cb) {
-            w[u][0] = ld_stream16(x + off[u]);
-            w[u][1] = ld_stream16(x + off[u] + 8);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            w[u][h] = make_uint4(0u, 0u, 0u, 0u);
+            if (rr[h] < rows && jj[h] < n_cb) w[u][h] = ld_stream16(x + rr[h] * cols + 64 * jj[h] + 16 * (k & 3) + 8 * hi);
         }
     }
     float g;
@@ -363,6 +396,7 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     const float yg = rcp_newton(g);
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
+        nv_pair_exchange(w[u][0], w[u][1]);  // now the lane's own block
         const float amax = as_f(amax16_to_f32_bits<IN>(max(amax16x8(w[u][0]), amax16x8(w[u][1]))));
         // the scale by the exact steps (valid when g and amax are within [2^-60, 2^60])
         const float cf = nvfp4_c_steps(amax, g, yg);
