@@ -657,7 +657,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
             if (rl >= rows) break;
             uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
             if (vec) {
-                *reinterpret_cast<v4u*>(o) = d;
+                __builtin_nontemporal_store(d, reinterpret_cast<v4u*>(o));
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e)

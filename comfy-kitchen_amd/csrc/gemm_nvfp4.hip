@@ -395,7 +395,7 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
             if (rl >= rows) break;
             uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
             if (vec) {
-                *reinterpret_cast<uint2*>(o) = d;
+                st_stream8(o, d);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
