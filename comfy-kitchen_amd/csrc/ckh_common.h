@@ -360,15 +360,48 @@ __device__ __forceinline__ float scale_of_amax_bits(uint32_t amax_bits, float in
     else return q;
 }
 
-// Workgroup-wide reduction of the partial words to the scale, for kernels that fuse pass 2
-// into their prologue.  Every thread of the workgroup (NT threads) must call it; `red`
-// is NT / 64 words of LDS.  The barrier waits for LDS traffic only, so global loads the
-// caller issued before stay in flight (except as the partial words' own loads require).
+// Raw buffer descriptor over [p, p + bytes): loads at offsets past `bytes` return 0.  The
+// address halves go through readfirstlane as unsigned 32-bit values (zero-extended when
+// the 64-bit base is rebuilt), so the descriptor lives in SGPRs.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+    const uint32_t n = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(bytes));
+    void* base = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | static_cast<uint64_t>(lo));
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(n), 0x00020000);
+}
+
+// Pass 2 fused into a kernel's prologue, in two steps.  load_partial_words issues the
+// thread's share of the (at most CKH_AMAX_WORKSPACE_BYTES / 4) partial words as
+// unconditional buffer loads (words past nparts read as 0): a caller that issues them
+// before its own data loads can later wait for them without waiting for its data, since
+// loads complete in order.  scale_from_partial_words then reduces them over the NT threads
+// of the workgroup (every thread must call it; `red` is NT / 64 words of LDS) to the
+// scale; its barrier waits for LDS traffic only.
+template <int NT>
+struct PartialWords {
+    static constexpr int N = (CKH_AMAX_WORKSPACE_BYTES / 4 + NT - 1) / NT;
+    uint32_t v[N];
+};
+
+template <int NT>
+__device__ __forceinline__ PartialWords<NT> load_partial_words(const uint32_t* __restrict__ partial,
+                                                               uint32_t nparts) {
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(partial, nparts * 4u);
+    PartialWords<NT> w;
+#pragma unroll
+    for (int i = 0; i < PartialWords<NT>::N; ++i)
+        w.v[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (threadIdx.x + i * NT) * 4u, 0, 0);
+    return w;
+}
+
 template <int IN, int NT>
-__device__ __forceinline__ float scale_from_partials(const uint32_t* __restrict__ partial, uint32_t nparts,
-                                                     float inv_divisor, uint32_t* red) {
-    uint32_t m = 0;
-    for (uint32_t i = threadIdx.x; i < nparts; i += NT) m = max(m, partial[i]);
+__device__ __forceinline__ float scale_from_partial_words(const PartialWords<NT>& w, float inv_divisor,
+                                                          uint32_t* red) {
+    uint32_t m = w.v[0];
+#pragma unroll
+    for (int i = 1; i < PartialWords<NT>::N; ++i) m = max(m, w.v[i]);
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, 64)));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
@@ -378,7 +411,7 @@ __device__ __forceinline__ float scale_from_partials(const uint32_t* __restrict_
     __asm__ volatile("" ::: "memory");
     uint32_t b = red[0];
 #pragma unroll
-    for (int w = 1; w < NT / 64; ++w) b = max(b, red[w]);
+    for (int i = 1; i < NT / 64; ++i) b = max(b, red[i]);
     return scale_of_amax_bits<IN>(b, inv_divisor);
 }
 

@@ -333,8 +333,9 @@ constexpr int kNvUnits = 2;  // units per thread: 2 passes cover a workgroup's 3
 // instruction reads 2 KB of one row.
 // DYN: the global scale is not an input but the layouts' default, amax(|x|) / divisor,
 // formed by every workgroup from the `nparts` partial maxima that amax_partials wrote for
-// this x (scale_from_partials); workgroup 0 stores it to *scale_out.  The x loads are
-// issued first, so their latency overlaps that reduction.
+// this x (scale_from_partial_words); workgroup 0 stores it to *scale_out.  The partial
+// words are loaded before the x data, so that reduction runs while the data loads are in
+// flight (measured: 35.4 -> 33.7 us on C5 against waiting for both).
 template <int IN, bool HI_FIRST, int G, bool DYN>
 __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint16_t* __restrict__ x,
                                                                      const float* __restrict__ gptr,
@@ -357,6 +358,14 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     const uint32_t l = threadIdx.x & 3;
     uint4 w[kNvUnits][2];
     uint32_t r[kNvUnits], off[kNvUnits], j[kNvUnits], ul[kNvUnits];
+    // DYN: the partial words first, then the data through a descriptor over this tile's
+    // rows (no conditional loads, so the wait for the partial words before the scale
+    // reduction leaves the data loads in flight)
+    PartialWords<64 * G> pw;
+    if constexpr (DYN) pw = load_partial_words<64 * G>(partial, nparts);
+    const uint32_t row0 = it.tile * 128;
+    __amdgpu_buffer_rsrc_t xrs;
+    if constexpr (DYN) xrs = buffer_rsrc(x + static_cast<size_t>(row0) * cols, min(rows - row0, 128u) * cols * 2u);
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         // The wave's 16 units (2 KB): A block k is block k of its first KB, B block k of
@@ -378,14 +387,23 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
         off[u] = r[u] * cols + 64 * j[u] + 16 * l;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            w[u][h] = make_uint4(0u, 0u, 0u, 0u);
-            if (rr[h] < rows && jj[h] < n_cb) w[u][h] = ld_stream16(x + rr[h] * cols + 64 * jj[h] + 16 * (k & 3) + 8 * hi);
+            const uint32_t e = 64 * jj[h] + 16 * (k & 3) + 8 * hi;  // element in the row
+            if constexpr (DYN) {
+                // rows past the end lie outside the descriptor, units past n_cb are sent there
+                const uint32_t bo = jj[h] < n_cb ? ((rr[h] - row0) * cols + e) * 2u : 0x80000000u;
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, bo, 0, 2);  // aux 2: nontemporal
+                w[u][h] = make_uint4(v[0], v[1], v[2], v[3]);
+            } else {
+                // (plain global loads measured 3.5% faster here than the buffer form)
+                w[u][h] = make_uint4(0u, 0u, 0u, 0u);
+                if (rr[h] < rows && jj[h] < n_cb) w[u][h] = ld_stream16(x + rr[h] * cols + e);
+            }
         }
     }
     float g;
     if constexpr (DYN) {
         __shared__ uint32_t red[G];
-        g = scale_from_partials<IN, 64 * G>(partial, nparts, inv_divisor, red);
+        g = scale_from_partial_words<IN, 64 * G>(pw, inv_divisor, red);
         if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = g;
     } else {
         g = gptr[0];
