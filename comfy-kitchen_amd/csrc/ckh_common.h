@@ -361,8 +361,10 @@ __device__ __forceinline__ float scale_of_amax_bits(uint32_t amax_bits, float in
 }
 
 // Raw buffer descriptor over [p, p + bytes): loads at offsets past `bytes` return 0.  The
-// address halves go through readfirstlane as unsigned 32-bit values (zero-extended when
-// the 64-bit base is rebuilt), so the descriptor lives in SGPRs.
+// inputs are wave-uniform by construction; reading them through readfirstlane keeps the
+// descriptor in SGPRs (a descriptor the compiler believes divergent turns every load into
+// a per-lane loop).  The address halves are taken as unsigned 32-bit values, so the low
+// half is zero-extended when the 64-bit base is rebuilt.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
     const uint64_t a = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));

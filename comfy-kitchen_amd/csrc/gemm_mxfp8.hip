@@ -96,18 +96,6 @@ __device__ __forceinline__ void for_each_index(Fn&& fn, std::integer_sequence<in
 
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
-// Buffer descriptor over [p, p + bytes).  The inputs are wave-uniform by construction;
-// reading them through readfirstlane keeps the descriptor in SGPRs (a descriptor the
-// compiler believes divergent turns every load into a per-lane loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
-    void* up = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(up, 0, static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
-                                             0x00020000);
-}
-
 struct Args {
     const uint8_t* a;   // activation [M, K]
     const uint8_t* b;   // weight [N, K]
@@ -145,7 +133,7 @@ struct Loader {
 __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int K, int wave, int lane,
                                              int rows_per_wave = 64) {
     Loader L;
-    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * K);
+    L.rs = buffer_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * K);
     const int row = rows_per_wave * wave + (lane >> 3), c = lane & 7;
     L.cbyte = c << 4;
     L.voff = static_cast<uint32_t>(row * K + L.cbyte);
@@ -215,7 +203,7 @@ struct Loader16 {
 __device__ __forceinline__ Loader16 make_loader16(const uint8_t* tile_base, int valid_rows, int K, int wave,
                                                   int lane) {
     Loader16 L;
-    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * 2u * K);
+    L.rs = buffer_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * 2u * K);
     const int row = 64 * wave + (lane >> 3), c = lane & 7;
     L.voff = static_cast<uint32_t>(row * 2 * K + 16 * c);
     L.rowstep = 16u * K;
@@ -421,8 +409,8 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // in-load quantize, waves 2, 3 repeat waves 0, 1 (identical bytes to the same LDS
     // words: a branch instead would let the compiler sink the MFMAs past the barriers)
     const int swave = AQ ? (wave & 1) : wave;
-    const __amdgpu_buffer_rsrc_t rssb = make_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
-    const __amdgpu_buffer_rsrc_t rssa = make_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
     const FragAddr faa = make_frag_addr(wm * 128, lane);
     const int KT = (p.K + BK - 1) / BK;

@@ -84,15 +84,6 @@ __device__ __forceinline__ void group_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
-    void* up = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-    return __builtin_amdgcn_make_buffer_rsrc(up, 0, static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)),
-                                             0x00020000);
-}
-
 struct Args {
     const uint8_t* a;
     const uint8_t* b;
@@ -121,7 +112,7 @@ struct Loader {
 
 __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int Kb, int wave, int lane) {
     Loader L;
-    L.rs = make_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * Kb);
+    L.rs = buffer_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * Kb);
     const int row = 64 * wave + (lane >> 3);
     L.cbyte = ((lane & 7) ^ (lane >> 3)) << 4;
     L.cdelta = static_cast<uint32_t>((L.cbyte ^ 16) - L.cbyte);
@@ -226,8 +217,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 
     const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * Kb, min(BN, p.N - n0), Kb, wave, lane);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * Kb, min(BM, p.M - m0), Kb, wave, lane);
-    const __amdgpu_buffer_rsrc_t rssb = make_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
-    const __amdgpu_buffer_rsrc_t rssa = make_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const int NG = (Kb + GKB - 1) / GKB;  // groups of 256 elements
 
     v16f acc[4][4];
