@@ -274,8 +274,8 @@ __global__ __launch_bounds__(kThreads) void quantize_nvfp4_kernel(const void* __
 // elements.  One lane per 16-element block, four lanes per unit (one scale word), two
 // units per thread.  A lane's block is two 16-byte chunks that another lane's loads
 // share (nv_pair_exchange), so that each load instruction reads one contiguous KB
-// rather than every other 16 bytes of 2 KB (which measured 6% slower).  The IEEE divisions of the
-// reference are replaced by Markstein correction steps, each exact:
+// rather than every other 16 bytes of 2 KB (which measured 6% slower).  The IEEE
+// divisions of the reference are replaced by Markstein correction steps, each exact:
 //   c = (amax / 6) / g:  c0 = amax*y6, c1 = fma(-fma(6, c0, -amax), y6, c0), then the
 //                        same step with y_g = RN(1/g) (one IEEE division per thread);
 //                        bit-identical to the two IEEE divisions for every bf16 / f16
@@ -365,7 +365,8 @@ __global__ __launch_bounds__(64 * G) void quantize_nvfp4_fast_kernel(const uint1
     if constexpr (DYN) pw = load_partial_words<64 * G>(partial, nparts);
     const uint32_t row0 = it.tile * 128;
     __amdgpu_buffer_rsrc_t xrs;
-    if constexpr (DYN) xrs = buffer_rsrc(x + static_cast<size_t>(row0) * cols, min(rows - row0, 128u) * cols * 2u);
+    if constexpr (DYN)
+        xrs = buffer_rsrc(x + static_cast<size_t>(row0) * cols, min(rows - row0, 128u) * cols * 2u);
 #pragma unroll
     for (int u = 0; u < kNvUnits; ++u) {
         // The wave's 16 units (2 KB): A block k is block k of its first KB, B block k of
