@@ -475,3 +475,18 @@ def test_quantize_nvfp4_dynamic_config5_activation(hip):
     q2, s2 = ck.quantize_nvfp4(ad, g.reshape(1))
     assert torch.equal(q, q2) and torch.equal(bits(s), bits(s2))
     _check_nv(a, g.cpu().reshape(1), pad=False)
+
+
+@pytest.mark.parametrize("m,k", [(32768, 768), (24576, 960)])
+def test_quantize_nvfp4_dynamic_many_partial_words(m, k, hip, seed):
+    """Narrow rows (cols < 1024: 256-thread quantize workgroups) with more amax partial
+    words than threads, so each thread reduces several of them: the fused path equals
+    amax_scale + quantize_nvfp4 on the device, and its scale equals torch's expression
+    evaluated on the device (tensor/nvfp4.py:65)."""
+    x = (torch.randn(m, k, device="cuda") * torch.exp(torch.randn(m, 1, device="cuda"))).bfloat16()
+    x[m // 2, 5] = 30000.0  # the maximum sits deep in the tensor
+    q, s, g = ck.quantize_nvfp4_dynamic(x, 2688.0)
+    want = (torch.amax(x.abs()) / 2688.0).float()
+    assert torch.equal(bits(g), bits(want)), (g.item(), want.item())
+    q2, s2 = ck.quantize_nvfp4(x, ck.amax_scale(x, 2688.0))
+    assert torch.equal(q, q2) and torch.equal(bits(s), bits(s2))
