@@ -22,7 +22,10 @@
 //
 // Pipeline: at stage t (after its barrier) the fragments of t are already in
 // registers; the LDS reads of stage t+1's fragments and scale words overlap stage t's
-// 16 MFMAs.  Global data moves in pairs of stages through registers: one load
+// 16 MFMAs.  Activation fragments are double-buffered (each is used by all of a stage's
+// MFMA rows); each weight fragment is read into its own registers right after its last
+// MFMA of the stage; with 32 fewer live VGPRs the block-scaled kernels no longer spill
+// (2 VGPRs still do in some per-tensor and bf16-activation instantiations).  Global data moves in pairs of stages through registers: one load
 // instruction brings whole 128-byte lines (both stages' halves of 8 rows).  An even
 // stage t writes the staged weight pair t+2, t+3 to LDS and loads the activation pair
 // t+4, t+5; the odd stage after it writes that pair and loads the next weight pair, so
@@ -284,10 +287,10 @@ __device__ __forceinline__ void store_scales(const ScaleWords& S, uint8_t* sx, u
     *reinterpret_cast<uint32_t*>(sy + off + 256) = S.s1;
 }
 
-template <int NW>
+// activation fragments of one stage (MFMA operand 1); the weight fragments (operand 0)
+// live in one v8i[NW] array
 struct Frags {
-    v8i b[NW];  // weight fragments (MFMA operand 0)
-    v8i a[4];   // activation fragments (MFMA operand 1)
+    v8i a[4];
 };
 
 // Byte offsets (within an operand tile) of this lane's two 16-byte fragment halves
@@ -314,11 +317,11 @@ __device__ __forceinline__ v8i read_frag(const uint8_t* tile, const FragAddr& f)
 }
 
 template <int NW>
-__device__ __forceinline__ void read_frags(Frags<NW>& F, const uint8_t* stage_buf, const FragAddr& fb,
+__device__ __forceinline__ void read_frags(Frags& F, v8i (&FB)[NW], const uint8_t* stage_buf, const FragAddr& fb,
                                            const FragAddr& fa) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        if (t < NW) F.b[t] = read_frag(stage_buf + t * 32 * BK, fb);
+        if (t < NW) FB[t] = read_frag(stage_buf + t * 32 * BK, fb);
         F.a[t] = read_frag(stage_buf + TILE + t * 32 * BK, fa);
     }
 }
@@ -470,10 +473,12 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     };
 
     uint32_t scb[4], sca[4];
-    Frags<NW> F0, F1;
+    Frags F0, F1;
+    v8i FB[NW];
 
-    // Stage t held in buffer B = t % 4 (compile-time): fragments F (stage t) are in
-    // registers; read stage t+1 into G.  A pair of stages (s, s+1), s even, moves in
+    // Stage t held in buffer B = t % 4 (compile-time): activation fragments F and the
+    // weight fragments FB (stage t) are in registers; read stage t+1 into G and, each
+    // after its last MFMA here (slot 4i + 3), into FB[i].  A pair of stages (s, s+1), s even, moves in
     // two halves: the activation pair is loaded at stage s-4 and written to LDS at
     // s-3, the weight pair (with scales) loaded at s-3 and written at s-2.  Each write
     // targets buffers whose previous stages were read before the current barrier.
@@ -482,8 +487,10 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // the order): the next stage's scale words first (their shifts 12 slots later, so
     // no LDS latency is exposed), then its fragments in the order the next stage uses
     // them, and in slots 0..7 one staged chunk written to LDS followed by the load that
-    // refills its registers, which therefore has a whole stage to arrive.
-    auto stage = [&](auto b_c, int t, Frags<NW>& F, Frags<NW>& G) {
+    // refills its registers, which therefore has a whole stage to arrive.  (Double-
+    // buffering the weight fragments too gave the same times, bit-identical, but spilled
+    // 2-3 VGPRs.)
+    auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
         constexpr int B = decltype(b_c)::value;
         constexpr bool EVEN = (B & 1) == 0;
         constexpr int OPSEL = EVEN ? 0 : 2;
@@ -501,16 +508,15 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         auto slot = [&](auto k_c) {
             constexpr int k = decltype(k_c)::value;
             constexpr int i = k / 4, j = k % 4;
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(F.b[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(FB[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
                                                                         OPSEL, sca[j]);
             if constexpr (k == 0 && !UNIT) {
                 wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + sbc * 512 + r32 * 16);
                 wa = *reinterpret_cast<const v4u*>(nx + 2 * TILE + STILE + wm * 512 + r32 * 16);
             }
             if constexpr (k == 1) G.a[0] = read_frag(nx + TILE, faa);
-            if constexpr (k == 2) G.b[0] = read_frag(nx, fab);
             if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
-            if constexpr (k >= 6 && k <= 4 + NW) G.b[k - 5] = read_frag(nx + (k - 5) * 32 * BK, fab);
+            if constexpr (k % 4 == 3 && k / 4 < NW) FB[k / 4] = read_frag(nx + (k / 4) * 32 * BK, fab);
             if constexpr (k < 8 && AQ) {
                 quantize_piece16<AIN, k, !EVEN>(LA16, SA, buf(P2{}) + TILE, buf(P2{}) + 2 * TILE + STILE, lane);
                 load_piece16<k>(LA16, SA, add16);
@@ -585,7 +591,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         store_pair(LA, XA, buf(B2{}) + TILE, buf(B3{}) + TILE);
     }
     stage_barrier<WAIT_LGKM0>();
-    read_frags(F0, lds01, fab, faa);
+    read_frags(F0, FB, lds01, fab, faa);
     read_scales(B0{}, scb, sca);
 
     // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
