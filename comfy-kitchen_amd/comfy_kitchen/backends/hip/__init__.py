@@ -50,7 +50,7 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_abi_version": (_i32, []),
     "ckh_last_error": (ctypes.c_char_p, []),
     "ckh_quantize_fp8": (_i32, [_p, _p, _p, _i64, _i32, _i32, _u64]),
-    "ckh_dequantize_fp8": (_i32, [_p, _p, _p, _i64, _i32, _i32, _u64]),
+    "ckh_dequantize_fp8": (_i32, [_p, _p, _p, _i64, _i32, _i32, _i32, _u64]),
     "ckh_quantize_mxfp8": (_i32, [_p, _p, _p, _i64, _i64, _i64, _i64, _i32, _u64]),
     "ckh_dequantize_mxfp8": (_i32, [_p, _p, _p, _i64, _i64, _i32, _u64]),
     "ckh_quantize_nvfp4": (_i32, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _u64]),
@@ -64,7 +64,7 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_quantize_nvfp4_dynamic": (_i32, [_p, _f32, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _p, _u64]),
     "ckh_scaled_mm_mxfp8_dynamic": (_i32, [_p] * 5 + [_i64] * 3 + [_i32] * 3 + [_u64]),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 # CKH_AMAX_WORKSPACE_BYTES of include/ckh.h: the workspace ckh_amax_scale takes
 AMAX_WORKSPACE_BYTES = 8192
 
@@ -135,6 +135,18 @@ def _scalar_on(t: torch.Tensor | float, device: torch.device, name: str) -> torc
     return t.reshape(1).contiguous()
 
 
+def _scalar_keep(t: torch.Tensor, device: torch.device, name: str) -> torch.Tensor:
+    """A one-element tensor of t's own float dtype on `device`: the kernel reads and widens
+    it, as eager's scale.to(out dtype) does."""
+    if not isinstance(t, torch.Tensor) or t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        return _scalar_on(t, device, name)
+    if t.numel() != 1:
+        raise ValueError(f"{name} must have exactly one element, got shape {tuple(t.shape)}")
+    if t.device != device:
+        t = t.to(device)
+    return t.reshape(1).contiguous()
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -146,7 +158,7 @@ def quantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
     s = _scalar_on(scale, x.device, "scale")
     out = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     with _on_device(x):
-        _call("ckh_quantize_fp8", x.data_ptr(), s.data_ptr(), out.data_ptr(), x.numel(),
+        _call("ckh_quantize_fp8", x.data_ptr(), out.data_ptr(), s.data_ptr(), x.numel(),
               DTYPE_TO_CODE[x.dtype], DTYPE_TO_CODE[output_type], _stream(x))
     return out.view(output_type)
 
@@ -154,11 +166,11 @@ def quantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
 def dequantize_per_tensor_fp8(x: torch.Tensor, scale: torch.Tensor,
                               output_type: torch.dtype = torch.bfloat16) -> torch.Tensor:
     x = x.contiguous()
-    s = _scalar_on(scale, x.device, "scale")
+    s = _scalar_keep(scale, x.device, "scale")
     out = torch.empty(x.shape, dtype=output_type, device=x.device)
     with _on_device(x):
-        _call("ckh_dequantize_fp8", x.data_ptr(), s.data_ptr(), out.data_ptr(), x.numel(),
-              DTYPE_TO_CODE[x.dtype], DTYPE_TO_CODE[output_type], _stream(x))
+        _call("ckh_dequantize_fp8", x.data_ptr(), out.data_ptr(), s.data_ptr(), x.numel(),
+              DTYPE_TO_CODE[x.dtype], DTYPE_TO_CODE[output_type], DTYPE_TO_CODE[s.dtype], _stream(x))
     return out
 
 
@@ -435,7 +447,7 @@ def _build_constraints() -> dict:
         "amax_scale": fc(x=ParamConstraint(dtypes=floats)),
         "quantize_per_tensor_fp8": fc(x=ParamConstraint(dtypes=floats), scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
                                       output_type=ParamConstraint(dtypes=fp8)),
-        "dequantize_per_tensor_fp8": fc(x=ParamConstraint(dtypes=fp8), scale=ParamConstraint(dtypes=f32, devices=frozenset({"cuda", "cpu"})),
+        "dequantize_per_tensor_fp8": fc(x=ParamConstraint(dtypes=fp8), scale=ParamConstraint(dtypes=floats, devices=frozenset({"cuda", "cpu"})),
                                         output_type=ParamConstraint(dtypes=floats)),
         "quantize_mxfp8": fc(x=ParamConstraint(dtypes=floats, shape_rules=two_d)),
         "dequantize_mxfp8": fc(qx=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
@@ -482,10 +494,10 @@ def _build_constraints() -> dict:
                               block_scale_b=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn})),
                               bias=ParamConstraint(dtypes=floats),
                               out_dtype=ParamConstraint(dtypes=floats)),
-        "apply_rope1": fc(x=ParamConstraint(dtypes=half, shape_rules=(ExactDims(4),)),
+        "apply_rope1": fc(x=ParamConstraint(dtypes=floats, shape_rules=(ExactDims(4),)),
                           freqs_cis=ParamConstraint(dtypes=floats, shape_rules=(ExactDims(6),))),
-        "apply_rope": fc(xq=ParamConstraint(dtypes=half, shape_rules=(ExactDims(4),)),
-                         xk=ParamConstraint(dtypes=half, shape_rules=(ExactDims(4),)),
+        "apply_rope": fc(xq=ParamConstraint(dtypes=floats, shape_rules=(ExactDims(4),)),
+                         xk=ParamConstraint(dtypes=floats, shape_rules=(ExactDims(4),)),
                          freqs_cis=ParamConstraint(dtypes=floats, shape_rules=(ExactDims(6),))),
     }
 

@@ -32,6 +32,32 @@ __device__ __forceinline__ uint32_t encode_fp8(float t) {
     }
 }
 
+// The code of a NaN product t = x * r, as the reference's eager arithmetic writes it
+// (torch's vectorised CPU kernels on x86; the c10 E4M3/E5M2 cast is 0x7F | sign for NaN):
+//  - bf16: the bf16 narrowing of the product (vec512_bfloat16.h cvtfp32_bf16) turns every
+//    NaN into 0xFFFF, so every NaN code is 0xFF.  (Eager's scalar remainder, the < 64
+//    elements of each thread's chunk past its last whole vector pair, narrows through
+//    c10::BFloat16 instead, whose NaN is 0x7FC0: 0x7F there.)
+//  - f16 / f32: the NaN keeps its sign through the multiply, clamp and narrowing.  The
+//    product's NaN is r's when r = 1/scale is NaN (scale NaN, r keeps its sign), else x's,
+//    else x86's default NaN, which is negative (0 * inf).
+template <int IN>
+__device__ __forceinline__ uint32_t fp8_nan_code(float x, float scale) {
+    if constexpr (IN == CKH_BF16) {
+        return 0xffu;
+    } else {
+        const uint32_t s = is_nan(scale) ? as_u(scale) : (is_nan(x) ? as_u(x) : 0x80000000u);
+        return 0x7fu | ((s >> 24) & 0x80u);
+    }
+}
+
+// One element through the reference's steps (software converts), NaN bytes included.
+template <int IN, int OUT>
+__device__ __forceinline__ uint32_t quantize_one(float x, float r, float scale) {
+    const float t = round_to<IN>(x * r);
+    return is_nan(t) ? fp8_nan_code<IN>(x, scale) : encode_fp8<OUT>(t);
+}
+
 template <int IN, int OUT, bool VEC>
 __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __restrict__ x,
                                                                 const float* __restrict__ scale,
@@ -46,7 +72,8 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
         // latencies overlap instead of adding up
         const Raw8<IN> ra = load8_raw<IN>(static_cast<const char*>(x) + ia * ES);
         const Raw8<IN> rb = load8_raw<IN>(static_cast<const char*>(x) + ib * ES);
-        const float r = round_to<IN>(1.0f / scale[0]);
+        const float sc = scale[0];
+        const float r = round_to<IN>(1.0f / sc);
         float v[16];
         unpack8<IN>(ra, *reinterpret_cast<float(*)[8]>(&v[0]));
         unpack8<IN>(rb, *reinterpret_cast<float(*)[8]>(&v[8]));
@@ -67,31 +94,32 @@ __global__ __launch_bounds__(kThreads) void quantize_fp8_kernel(const void* __re
             for (int b = 0; b < 4; ++b) c[b] = __builtin_amdgcn_fmed3f(t[4 * q + b], -MX, MX);
             w[q] = OUT == CKH_E4M3 ? hw_e4m3x4(c[0], c[1], c[2], c[3]) : hw_e5m2x4(c[0], c[1], c[2], c[3]);
         }
-        if (any_nan) {  // keep the software's NaN bytes
+        if (any_nan) {  // the reference's NaN bytes (fp8_nan_code)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 uint32_t acc = 0;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
+                for (int b = 0; b < 4; ++b) acc |= quantize_one<IN, OUT>(v[4 * q + b], r, sc) << (8 * b);
                 w[q] = acc;
             }
         }
         st_stream8(out + ia, make_uint2(w[0], w[1]));
         st_stream8(out + ib, make_uint2(w[2], w[3]));
     } else {
-        const float r = round_to<IN>(1.0f / scale[0]);
+        const float sc = scale[0];
+        const float r = round_to<IN>(1.0f / sc);
         for (int64_t i = ia; i < n && i < ia + 8; ++i)
-            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+            out[i] = static_cast<uint8_t>(quantize_one<IN, OUT>(load1<IN>(x, i), r, sc));
         for (int64_t i = ib; i < n && i < ib + 8; ++i)
-            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+            out[i] = static_cast<uint8_t>(quantize_one<IN, OUT>(load1<IN>(x, i), r, sc));
     }
 }
 
 // One wave-tile (1024 elements; lane l: pieces l and 64 + l) of the quantizer from its
 // raw loads: codes stored, a NaN-containing lane re-encoded by the software path.
 template <int IN, int OUT>
-__device__ __forceinline__ void quantize_tile(const Raw8<IN>& ra, const Raw8<IN>& rb, float r, uint8_t* out,
-                                              int64_t ia, int64_t ib) {
+__device__ __forceinline__ void quantize_tile(const Raw8<IN>& ra, const Raw8<IN>& rb, float r, float sc,
+                                              uint8_t* out, int64_t ia, int64_t ib) {
     float v[16];
     unpack8<IN>(ra, *reinterpret_cast<float(*)[8]>(&v[0]));
     unpack8<IN>(rb, *reinterpret_cast<float(*)[8]>(&v[8]));
@@ -111,12 +139,12 @@ __device__ __forceinline__ void quantize_tile(const Raw8<IN>& ra, const Raw8<IN>
         for (int b = 0; b < 4; ++b) c[b] = __builtin_amdgcn_fmed3f(t[4 * q + b], -MX, MX);
         w[q] = OUT == CKH_E4M3 ? hw_e4m3x4(c[0], c[1], c[2], c[3]) : hw_e5m2x4(c[0], c[1], c[2], c[3]);
     }
-    if (any_nan) {  // keep the software's NaN bytes
+    if (any_nan) {  // the reference's NaN bytes (fp8_nan_code)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             uint32_t acc = 0;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) acc |= encode_fp8<OUT>(round_to<IN>(v[4 * q + b] * r)) << (8 * b);
+            for (int b = 0; b < 4; ++b) acc |= quantize_one<IN, OUT>(v[4 * q + b], r, sc) << (8 * b);
             w[q] = acc;
         }
     }
@@ -149,7 +177,8 @@ __global__ __launch_bounds__(256) void quantize_fp8_pipe_kernel(const void* __re
         ra = load8_raw<IN>(xb + (static_cast<int64_t>(t) * 1024 + 8 * lane) * ES);
         rb = load8_raw<IN>(xb + (static_cast<int64_t>(t) * 1024 + 512 + 8 * lane) * ES);
     }
-    const float r = round_to<IN>(1.0f / scale[0]);
+    const float sc = scale[0];
+    const float r = round_to<IN>(1.0f / sc);
     while (t < tiles) {
         const uint32_t tn = t + W;
         Raw8<IN> na = ra, nb = rb;
@@ -158,14 +187,14 @@ __global__ __launch_bounds__(256) void quantize_fp8_pipe_kernel(const void* __re
             nb = load8_raw<IN>(xb + (static_cast<int64_t>(tn) * 1024 + 512 + 8 * lane) * ES);
         }
         const int64_t ia = static_cast<int64_t>(t) * 1024 + 8 * lane;
-        quantize_tile<IN, OUT>(ra, rb, r, out, ia, ia + 512);
+        quantize_tile<IN, OUT>(ra, rb, r, sc, out, ia, ia + 512);
         t = tn;
         ra = na;
         rb = nb;
     }
     if (w0 == 0) {
         for (int64_t i = static_cast<int64_t>(tiles) * 1024 + lane; i < n; i += 64)
-            out[i] = static_cast<uint8_t>(encode_fp8<OUT>(round_to<IN>(load1<IN>(x, i) * r)));
+            out[i] = static_cast<uint8_t>(quantize_one<IN, OUT>(load1<IN>(x, i), r, sc));
     }
 }
 
@@ -229,9 +258,17 @@ __device__ __forceinline__ void store16(void* out, int64_t i, int64_t j, const f
     }
 }
 
+// The scale as eager reads it, scale.to(out dtype): widened to fp32 from its own dtype
+// (exact), then rounded to the output dtype.
+__device__ __forceinline__ float load_scale(const void* p, int code) {
+    if (code == CKH_F32) return *static_cast<const float*>(p);
+    const uint32_t h = *static_cast<const uint16_t*>(p);
+    return code == CKH_BF16 ? bf16_to_f(h) : f16_to_f(h);
+}
+
 template <int IN, int OUT, bool VEC>
 __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t* __restrict__ x,
-                                                                  const float* __restrict__ scale,
+                                                                  const void* __restrict__ scale, int scale_code,
                                                                   void* __restrict__ out, int64_t n) {
     // a wave's 1024 codes: lane l takes the 8-code pieces l and 64 + l, so every load and
     // store instruction covers one contiguous run
@@ -242,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
         // the code loads go out before the scale is read and rounded
         const u32x2 ca = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ia));
         const u32x2 cb = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + ib));
-        const float s = round_to<OUT>(scale[0]);
+        const float s = round_to<OUT>(load_scale(scale, scale_code));
         uint32_t cw[4] = {ca.x, ca.y, cb.x, cb.y};
         // a NaN code (0x7f / 0xff in E4M3) takes the software path, which fixes its bytes
         bool nan_code = false;
@@ -268,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_fp8_kernel(const uint8_t*
             store16<OUT>(out, ia, ib, v);
         }
     } else {
-        const float s = round_to<OUT>(scale[0]);
+        const float s = round_to<OUT>(load_scale(scale, scale_code));
         for (int64_t i = ia; i < n && i < ia + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
         for (int64_t i = ib; i < n && i < ib + 8; ++i) store_out<OUT>(out, i, decode_fp8<IN>(x[i]) * s);
     }
@@ -289,7 +326,7 @@ using namespace ckh;
         }                           \
     } while (0)
 
-extern "C" int ckh_quantize_fp8(const void* x, const void* scale, void* out, int64_t numel, int in_code,
+extern "C" int ckh_quantize_fp8(const void* x, void* out, const void* scale, int64_t numel, int in_code,
                                 int out_code, uintptr_t stream) {
     CKH_REQUIRE(numel >= 0, "quantize_fp8: numel < 0");
     if (numel == 0) return CKH_OK;
@@ -339,8 +376,8 @@ extern "C" int ckh_quantize_fp8(const void* x, const void* scale, void* out, int
     return check_launch("quantize_fp8");
 }
 
-extern "C" int ckh_dequantize_fp8(const void* x, const void* scale, void* out, int64_t numel, int in_code,
-                                  int out_code, uintptr_t stream) {
+extern "C" int ckh_dequantize_fp8(const void* x, void* out, const void* scale, int64_t numel, int in_code,
+                                  int out_code, int scale_code, uintptr_t stream) {
     CKH_REQUIRE(numel >= 0, "dequantize_fp8: numel < 0");
     if (numel == 0) return CKH_OK;
     CKH_REQUIRE(x && scale && out, "dequantize_fp8: null pointer");
@@ -348,14 +385,16 @@ extern "C" int ckh_dequantize_fp8(const void* x, const void* scale, void* out, i
                 in_code);
     CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
                 "dequantize_fp8: unsupported output dtype code %d", out_code);
+    CKH_REQUIRE(scale_code == CKH_F32 || scale_code == CKH_F16 || scale_code == CKH_BF16,
+                "dequantize_fp8: unsupported scale dtype code %d", scale_code);
+    CKH_REQUIRE(aligned(scale, scale_code == CKH_F32 ? 4 : 2), "dequantize_fp8: scale misaligned");
     const bool vec = aligned(x, 16) && aligned(out, 16);
     dim3 grid(static_cast<unsigned>(cdiv(numel, kThreads * kPerThread)));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const float* sp = static_cast<const float*>(scale);
     const uint8_t* xi = static_cast<const uint8_t*>(x);
 #define LAUNCH_DQ(I, O)                                                                               \
     CKH_DISPATCH_VEC(vec, hipLaunchKernelGGL((dequantize_fp8_kernel<I, O, V>), grid, dim3(kThreads), 0, st, \
-                                             xi, sp, out, numel))
+                                             xi, scale, scale_code, out, numel))
     if (in_code == CKH_E4M3) {
         if (out_code == CKH_F32) LAUNCH_DQ(CKH_E4M3, CKH_F32);
         else if (out_code == CKH_F16) LAUNCH_DQ(CKH_E4M3, CKH_F16);

@@ -56,11 +56,13 @@ __device__ __forceinline__ uint2 mx_encode8(const float (&v)[8], uint32_t amax_b
     uint32_t w[2] = {0u, 0u};
     if (amax_bits == 0) return make_uint2(0u, 0u);  // zero block: +0 codes
     if (e == 0) {
-        // Scale 0.0: x/0 is +-inf (clamped to +-448) for x != 0 and NaN for x == 0.
+        // Scale 0.0 (eager's fp32 division on x86): x/0 is +-inf, clamped to +-448, for
+        // non-NaN x != 0 (inf included); 0/0 is x86's default NaN, which is negative
+        // (0xFF); a NaN x stays x's NaN, sign kept (0x7F | sign).
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            uint32_t a = as_u(v[t]) & 0x7fffffffu;
-            uint32_t c = (a == 0 || a > 0x7f800000u) ? 0xffu : (0x7eu | ((as_u(v[t]) >> 24) & 0x80u));
+            const uint32_t u = as_u(v[t]), a = u & 0x7fffffffu, sign = (u >> 24) & 0x80u;
+            const uint32_t c = a == 0 ? 0xffu : (a > 0x7f800000u ? (0x7fu | sign) : (0x7eu | sign));
             w[t >> 2] |= c << (8 * (t & 3));
         }
         return make_uint2(w[0], w[1]);

@@ -42,9 +42,11 @@ __device__ __forceinline__ float ld(const void* p, int64_t i) {
     return load1<C>(p, i);
 }
 
+// The output value of x's dtype as its bits (fp32 x: the value itself).
 template <int XC>
 __device__ __forceinline__ uint32_t to_bits(float f) {
-    return XC == CKH_BF16 ? f_to_bf16(f) : f_to_f16(f);
+    if constexpr (XC == CKH_F32) return as_u(f);
+    else return XC == CKH_BF16 ? f_to_bf16(f) : f_to_f16(f);
 }
 
 template <int XC, int FC, int PPL>
@@ -91,9 +93,10 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
             const void* src = which ? a.xk : a.xq;
             void* dst = which ? a.ok : a.oq;
             if (src == nullptr) break;
+            constexpr int ES = ElemSize<XC>::value;
             float x[2 * PPL];
             if constexpr (PPL == 4) {
-                load8<XC>(static_cast<const uint16_t*>(src) + xoff, x);
+                load8<XC>(static_cast<const char*>(src) + xoff * ES, x);
             } else {
 #pragma unroll
                 for (int e = 0; e < 2 * PPL; ++e) x[e] = ld<XC>(src, xoff + e);
@@ -109,13 +112,24 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
                     o[2 * i + r] = to_bits<XC>(y);
                 }
             }
-            uint16_t* op = static_cast<uint16_t*>(dst) + ooff;
-            if constexpr (PPL == 4) {
-                *reinterpret_cast<uint4*>(op) =
-                    make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
-            } else {
+            if constexpr (XC == CKH_F32) {
+                uint32_t* op = static_cast<uint32_t*>(dst) + ooff;
+                if constexpr (PPL == 4) {
+                    *reinterpret_cast<uint4*>(op) = make_uint4(o[0], o[1], o[2], o[3]);
+                    *reinterpret_cast<uint4*>(op + 4) = make_uint4(o[4], o[5], o[6], o[7]);
+                } else {
 #pragma unroll
-                for (int e = 0; e < 2 * PPL; ++e) op[e] = static_cast<uint16_t>(o[e]);
+                    for (int e = 0; e < 2 * PPL; ++e) op[e] = o[e];
+                }
+            } else {
+                uint16_t* op = static_cast<uint16_t*>(dst) + ooff;
+                if constexpr (PPL == 4) {
+                    *reinterpret_cast<uint4*>(op) = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16),
+                                                               o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2 * PPL; ++e) op[e] = static_cast<uint16_t>(o[e]);
+                }
             }
         }
     }
@@ -293,7 +307,8 @@ extern "C" int ckh_apply_rope(const void* xq, const void* xk, const void* freqs,
     CKH_REQUIRE(batch >= 0 && dim1 >= 0 && dim2 >= 0, "apply_rope: negative shape");
     CKH_REQUIRE(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 4096, "apply_rope: head_dim (%lld) must be even",
                 (long long)head_dim);
-    CKH_REQUIRE(in_code == CKH_F16 || in_code == CKH_BF16, "apply_rope: unsupported x dtype code %d", in_code);
+    CKH_REQUIRE(in_code == CKH_F32 || in_code == CKH_F16 || in_code == CKH_BF16,
+                "apply_rope: unsupported x dtype code %d", in_code);
     CKH_REQUIRE(freqs_code == CKH_F32 || freqs_code == CKH_F16 || freqs_code == CKH_BF16,
                 "apply_rope: unsupported freqs dtype code %d", freqs_code);
     CKH_REQUIRE(freqs_batch == 1 || freqs_batch == batch, "apply_rope: freqs dim 0 (%lld) does not broadcast to %lld",
@@ -323,7 +338,8 @@ extern "C" int ckh_apply_rope(const void* xq, const void* xk, const void* freqs,
     // 16-byte freqs loads: f32 rows are covered by vec; 16-bit rows need it here
     const bool fvec = freqs_code == CKH_F32 ||
                       (aligned(freqs, 16) && sf_batch % 8 == 0 && sf_dim1 % 8 == 0 && sf_dim2 % 8 == 0);
-    if (vec && fvec && lanes <= 64 && (64 % lanes) == 0 && P < (int64_t(1) << 30) && a.R < (int64_t(1) << 30)) {
+    if (in_code != CKH_F32 && vec && fvec && lanes <= 64 && (64 % lanes) == 0 && P < (int64_t(1) << 30) &&
+        a.R < (int64_t(1) << 30)) {
         RopeWaveArgs w{};
         w.xq = xq; w.xk = xk; w.freqs = freqs; w.oq = xq_out; w.ok = xk_out;
         w.D1 = dim1; w.D2 = dim2;
@@ -382,7 +398,8 @@ extern "C" int ckh_apply_rope(const void* xq, const void* xk, const void* freqs,
         else BY_PPL(XC, CKH_BF16);                      \
     } while (0)
     if (in_code == CKH_BF16) BY_FC(CKH_BF16);
-    else BY_FC(CKH_F16);
+    else if (in_code == CKH_F16) BY_FC(CKH_F16);
+    else BY_FC(CKH_F32);
 #undef BY_FC
 #undef BY_PPL
 #undef LAUNCH

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 6
+#define CKH_ABI_VERSION 7
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -59,20 +59,26 @@ const char* ckh_last_error(void);
  * Per-tensor FP8 quantize: out = fp8(clamp(x * r, +-max)), r = (1/scale) rounded to
  * x's dtype, the product rounded to x's dtype, then round-to-nearest-even to FP8.
  * x: numel elements of in_code (f32/f16/bf16); scale: one f32 on device;
- * out: numel bytes of out_code (e4m3 / e5m2).
+ * out: numel bytes of out_code (e4m3 / e5m2).  A NaN product gives the byte eager's
+ * vectorised CPU loop writes: 0xFF for bf16 x; 0x7F | sign for f16 / f32 x (the sign of
+ * r's NaN, else of x's NaN, else negative for 0 * inf).
  * Replaces launch_quantize_fp8_kernel (reference backends/cuda/dlpack_bindings.cpp:45-48,
- * ops/per_tensor_quantize.cu:170-209); arithmetic follows backends/eager/quantization.py:41-55.
+ * ops/per_tensor_quantize.cu:170-209), with the same argument order; arithmetic follows
+ * backends/eager/quantization.py:41-55.
  */
-int ckh_quantize_fp8(const void* x, const void* scale, void* out, int64_t numel,
+int ckh_quantize_fp8(const void* x, void* out, const void* scale, int64_t numel,
                      int in_code, int out_code, uintptr_t stream);
 
 /*
  * Per-tensor FP8 dequantize: out = x.to(out) * scale.to(out), rounded to out_code.
+ * scale: one element of scale_code (f32 / f16 / bf16) on device, as eager accepts it.
  * Replaces launch_dequantize_fp8_kernel (dlpack_bindings.cpp:50-53,
- * ops/per_tensor_quantize.cu:211-249); arithmetic follows eager quantization.py:57-61.
+ * ops/per_tensor_quantize.cu:211-249): the same arguments in the same order, plus
+ * scale_code before the stream (that launcher reads an f32 scale only); arithmetic
+ * follows eager quantization.py:57-61.
  */
-int ckh_dequantize_fp8(const void* x, const void* scale, void* out, int64_t numel,
-                       int in_code, int out_code, uintptr_t stream);
+int ckh_dequantize_fp8(const void* x, void* out, const void* scale, int64_t numel,
+                       int in_code, int out_code, int scale_code, uintptr_t stream);
 
 /*
  * MXFP8 quantize of x [orig_rows, orig_cols] (row-major, in_code f32/f16/bf16) into
@@ -121,6 +127,7 @@ int ckh_dequantize_nvfp4(const void* qx, const void* global_scale, const void* s
  * three dims; the inner [head_dim/2, 2, 2] must be contiguous).  A freqs dim of size 1
  * broadcasts; otherwise it must equal x's (dim 2 may be longer and is then truncated).
  * out_i = f[i,0]*x0 + f[i,1]*x1 per pair, computed in the freqs dtype, rounded to x's.
+ * x: in_code f32 / f16 / bf16; freqs: freqs_code f32 / f16 / bf16.
  * xk / xk_out may be NULL (apply_rope1).  Outputs are contiguous [batch,dim1,dim2,hd].
  * Replaces launch_apply_rope_kernel (dlpack_bindings.cpp:76-102,
  * ops/apply_rope.cu:317-362); arithmetic follows eager rope.py:7-18.
@@ -183,6 +190,11 @@ int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const 
  * K % 32 == 0.
  * Replaces launch_cublas_gemm_blockwise_fp4_kernel (dlpack_bindings.cpp:59-74,
  * ops/cublas_gemm_nvfp4.cu:297-342); semantics follow eager quantization.py:222-246.
+ * Argument differences from that launcher: the activation comes first (the launcher takes
+ * B before A because cuBLASLt is column-major; the product is the same A B^T); there is no
+ * workspace (nothing is allocated or needed) and no `accumulate` flag (its only caller,
+ * backends/cuda/__init__.py:353, always passes false, i.e. out is overwritten); bias_code
+ * names the bias dtype, which that launcher takes from the DLPack tensor.
  */
 int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void* sb,
                         const void* alpha, const void* bias, void* out, int64_t M,

@@ -50,15 +50,16 @@ static int nearest_code(double ax, int maxcode, double (*val)(int)) {
     return best;
 }
 
-/* x already clamped to [-448, 448] or NaN; NaN -> 0xFF */
+/* x already clamped to [-448, 448] or NaN.  A NaN keeps its sign: 0x7F | sign, the
+ * rule of torch's c10 fp32 -> Float8_e4m3fn / Float8_e5m2 conversion. */
 int ref_f32_to_e4m3(float x) {
-    if (isnan(x)) return 0xff;
+    if (isnan(x)) return signbit(x) ? 0xff : 0x7f;
     int c = nearest_code(fabs((double)x), 0x7e, ref_e4m3_value);
     return (signbit(x) ? 0x80 : 0) | c;
 }
 
 int ref_f32_to_e5m2(float x) {
-    if (isnan(x)) return 0xff;
+    if (isnan(x)) return signbit(x) ? 0xff : 0x7f;
     int c = nearest_code(fabs((double)x), 0x7b, ref_e5m2_value);
     return (signbit(x) ? 0x80 : 0) | c;
 }
@@ -84,12 +85,21 @@ uint16_t ref_f32_to_bf16(float x) {
 
 float ref_bf16_value(uint16_t h) { return f_from_bits((uint32_t)h << 16); }
 
-/* ---- per-tensor FP8 on bf16 input (quantization.py:53-55) */
+/* bf16 narrowing in torch's vectorised CPU kernels (x86 vec256/vec512 cvtfp32_bf16):
+ * round to nearest even, and every NaN becomes 0xFFFF. */
+uint16_t ref_vec_f32_to_bf16(float x) {
+    if (isnan(x)) return 0xffff;
+    return ref_f32_to_bf16(x);
+}
+
+/* ---- per-tensor FP8 on bf16 input (quantization.py:53-55), as eager's vectorised
+ * loop computes it: the bf16 product is narrowed by ref_vec_f32_to_bf16, so every NaN
+ * product encodes as 0xFF.  (r is a one-element tensor, narrowed by c10::BFloat16.) */
 void ref_quantize_fp8_bf16(const uint16_t* x, int64_t n, float scale, int e5m2, uint8_t* out) {
     float r = ref_bf16_value(ref_f32_to_bf16(1.0f / scale));
     float lim = e5m2 ? 57344.0f : 448.0f;
     for (int64_t i = 0; i < n; ++i) {
-        float t = ref_bf16_value(ref_f32_to_bf16(ref_bf16_value(x[i]) * r));
+        float t = ref_bf16_value(ref_vec_f32_to_bf16(ref_bf16_value(x[i]) * r));
         if (t > lim) t = lim;
         if (t < -lim) t = -lim;
         out[i] = (uint8_t)(e5m2 ? ref_f32_to_e5m2(t) : ref_f32_to_e4m3(t));

@@ -7,7 +7,6 @@ from pathlib import Path
 import torch
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "known_answers.json"
-NAN = "nan"
 
 
 def _load() -> dict:
@@ -15,7 +14,7 @@ def _load() -> dict:
 
 
 def _code(s):
-    return NAN if s == NAN else int(s, 16)
+    return int(s, 16)
 
 
 def _expand(spec: dict, n: int, conv) -> list:
@@ -25,13 +24,30 @@ def _expand(spec: dict, n: int, conv) -> list:
     return out
 
 
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+BITS_VIEW = {torch.bfloat16: torch.int16, torch.float16: torch.int16, torch.float32: torch.int32}
+VEC_LEN = 64  # per-tensor FP8 cases fill a tensor of this many elements (eager's vectorised loop)
+
+
+def _from_bits(hexbits: str, dtype: torch.dtype, n: int) -> torch.Tensor:
+    v = int(hexbits, 16)
+    width = 32 if dtype == torch.float32 else 16
+    if v >= 1 << (width - 1):
+        v -= 1 << width
+    return torch.full((n,), v, dtype=BITS_VIEW[dtype]).view(dtype)
+
+
 def fp8_quant_cases():
-    """(x bf16 [1], scale f32 [1], output dtype, expected code)"""
+    """(x [64] of the case's dtype, every element the case's value; scale f32 [1]; output
+    dtype; expected code of every element)"""
     res = []
     for c in _load()["quantize_per_tensor_fp8"]:
         dt = torch.float8_e4m3fn if c["out"] == "e4m3" else torch.float8_e5m2
-        res.append((torch.tensor([c["x"]], dtype=torch.bfloat16), torch.tensor([c["scale"]], dtype=torch.float32),
-                    dt, int(c["code"], 16)))
+        xdt = DTYPES[c.get("dtype", "bf16")]
+        x = _from_bits(c["x_bits"], xdt, VEC_LEN) if "x_bits" in c else torch.full((VEC_LEN,), c["x"], dtype=xdt)
+        s = (_from_bits(c["scale_bits"], torch.float32, 1) if "scale_bits" in c
+             else torch.tensor([c["scale"]], dtype=torch.float32))
+        res.append((x, s, dt, int(c["code"], 16)))
     return res
 
 
@@ -45,10 +61,12 @@ def fp8_dequant_cases():
 
 
 def mxfp8_cases():
-    """(block bf16 [32], expected scale byte, expected codes list[int | 'nan'])"""
+    """(block bf16 [32], expected scale byte, expected codes list[int])"""
     res = []
     for c in _load()["quantize_mxfp8"]:
         x = torch.tensor(_expand(c["block"], 32, float), dtype=torch.bfloat16)
+        for k, v in c.get("block_bits", {}).items():
+            x[int(k)] = _from_bits(v, torch.bfloat16, 1)[0]
         res.append((x, int(c["scale"], 16), _expand(c["codes"], 32, _code)))
     return res
 
@@ -63,15 +81,9 @@ def nvfp4_cases():
     return res
 
 
-def codes_match(got: list[int], want: list) -> bool:
-    """Byte-wise compare where 'nan' accepts either FP8 NaN code."""
-    for g, w in zip(got, want):
-        if w == NAN:
-            if g & 0x7F != 0x7F:
-                return False
-        elif g != w:
-            return False
-    return len(got) == len(want)
+def codes_match(got: list[int], want: list[int]) -> bool:
+    """Byte-wise compare, NaN code bytes included (sign and all)."""
+    return list(got) == list(want)
 
 
 def unpack(packed: torch.Tensor, hi_first: bool = True) -> list[int]:

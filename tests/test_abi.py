@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 6
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 7
 
 
 def test_amax_workspace_size_matches_header():
@@ -47,6 +47,10 @@ def test_invalid_arguments_return_error(lib):
     p = ctypes.addressof(buf)
     assert lib.ckh_quantize_fp8(p, p, p, 16, 7, 5, 0) == 1
     assert b"unsupported input dtype" in lib.ckh_last_error()
+    assert lib.ckh_dequantize_fp8(p, p, p, 16, 5, 2, 5, 0) == 1
+    assert b"unsupported scale dtype" in lib.ckh_last_error()
+    assert lib.ckh_apply_rope(p, None, p, p, None, 1, 1, 1, 128, 1, 1, 1, 128, 128, 128, 256, 256, 256, 5, 0, 0) == 1
+    assert b"unsupported x dtype" in lib.ckh_last_error()
     assert lib.ckh_quantize_mxfp8(p, p, p, 4, 48, 4, 48, 2, 0) == 1
     assert b"multiple of 32" in lib.ckh_last_error()
     assert lib.ckh_apply_rope(p, None, p, p, p, 1, 1, 1, 128, 1, 1, 1, 128, 128, 128, 256, 256, 256, 2, 0, 0) == 1
@@ -72,7 +76,7 @@ def test_invalid_arguments_return_error(lib):
 
 def test_zero_sized_calls_are_noops(lib):
     assert lib.ckh_quantize_fp8(None, None, None, 0, 2, 5, 0) == 0
-    assert lib.ckh_dequantize_fp8(None, None, None, 0, 5, 2, 0) == 0
+    assert lib.ckh_dequantize_fp8(None, None, None, 0, 5, 2, 0, 0) == 0
 
 
 def test_quantize_nvfp4_dynamic_rejects_bad_arguments(lib):

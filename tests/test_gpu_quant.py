@@ -1,9 +1,11 @@
 """HIP quantizers / dequantizers vs the CPU oracle: bit-exact codes, scales and outputs.
 
 Bar: every code byte, every scale byte (including swizzle padding) and every
-dequantized element equal to the oracle's (the reference eager arithmetic).  NaN
-results compare as NaN-equivalent (any NaN code), since the reference's own CPU paths
-emit either NaN encoding.
+dequantized element equal to the oracle's (the reference eager arithmetic).  Quantized
+NaN code bytes compare exactly.  Inputs holding NaNs are sized in multiples of 64
+elements, so that eager's vectorised loop alone produces them (its scalar remainder
+writes other NaN bytes for bf16 input; the kernels follow the vectorised loop).
+Dequantized NaN values compare by position: their payload bits are the device's.
 """
 import pytest
 import torch
@@ -17,14 +19,12 @@ pytestmark = pytest.mark.gpu
 
 
 def _fp8_equal(got: torch.Tensor, want: torch.Tensor, dt=torch.float8_e4m3fn):
+    """Every code byte equal, NaN codes included (sign and all)."""
     g, w = bits(got).reshape(-1), bits(want).reshape(-1)
-    if dt == torch.float8_e4m3fn:
-        gn, wn = (g & 0x7F) == 0x7F, (w & 0x7F) == 0x7F
-    else:
-        gn, wn = (g & 0x7F) > 0x7C, (w & 0x7F) > 0x7C
-    assert torch.equal(gn, wn), f"NaN positions differ: {int((gn != wn).sum())}"
-    bad = (g != w) & ~wn
-    assert int(bad.sum()) == 0, f"{int(bad.sum())} of {g.numel()} codes differ; first at {bad.nonzero()[:5].flatten().tolist()}"
+    bad = g != w
+    assert int(bad.sum()) == 0, (f"{int(bad.sum())} of {g.numel()} codes differ; first at "
+                                 f"{bad.nonzero()[:5].flatten().tolist()}: got {g[bad][:5].tolist()}, "
+                                 f"want {w[bad][:5].tolist()}")
 
 
 # ------------------------------------------------------------- known answers
@@ -32,7 +32,7 @@ def _fp8_equal(got: torch.Tensor, want: torch.Tensor, dt=torch.float8_e4m3fn):
 def test_kat_quantize_fp8(case, hip, dev):
     x, scale, dt, want = kat.fp8_quant_cases()[case]
     got = ck.quantize_per_tensor_fp8(x.to(dev), scale.to(dev), dt)
-    assert bits(got).item() == want
+    assert bits(got).tolist() == [want] * x.numel()
 
 
 @pytest.mark.parametrize("case", range(len(kat.fp8_dequant_cases())))
@@ -73,6 +73,41 @@ def test_quantize_fp8_every_bf16(scale, out_dtype, hip, dev):
     _fp8_equal(got, want, out_dtype)
 
 
+def _nan_mix(dtype: torch.dtype, n: int, gen: torch.Generator) -> torch.Tensor:
+    """n values of dtype: finite values, +-0, +-inf and NaNs of both signs, shuffled."""
+    x = (torch.randn(n, generator=gen) * 30).to(dtype)
+    pos, neg = {torch.bfloat16: (0x7FC0, -0x40), torch.float16: (0x7E00, -0x200),
+                torch.float32: (0x7FC00000, -0x400000)}[dtype]
+    xb = x.view(kat.BITS_VIEW[dtype])
+    idx = torch.randperm(n, generator=gen)
+    q = n // 8
+    xb[idx[:q]] = pos
+    xb[idx[q:2 * q]] = neg
+    x[idx[2 * q:2 * q + q // 2]] = 0.0
+    x[idx[2 * q + q // 2:3 * q]] = -0.0
+    x[idx[3 * q:3 * q + q // 2]] = float("inf")
+    x[idx[3 * q + q // 2:4 * q]] = -float("inf")
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("scale_bits", [0x3F800000, 0x3E000000, 0x00000000, 0x7F800000, 0x7FC00000, -0x400000],
+                         ids=["1", "0.125", "0", "inf", "nan", "-nan"])
+@pytest.mark.parametrize("n", [64, 4096, 5184])
+def test_quantize_fp8_nan_bytes(dtype, out_dtype, scale_bits, n, hip, dev):
+    """NaN code bytes exactly as eager writes them (vectorised loop: n is a multiple of 64),
+    for NaN inputs of both signs, 0 * inf, and NaN / zero / infinite scales; 4096 and 5184
+    elements take the persistent kernel (16-bit input; 5184 leaves a remainder past the
+    last 1024-element tile) or the vector kernel (fp32), 64 the scalar path."""
+    g = torch.Generator().manual_seed(n + scale_bits)
+    x = _nan_mix(dtype, n, g)
+    scale = torch.tensor([scale_bits], dtype=torch.int32).view(torch.float32)
+    want = ref.quantize_per_tensor_fp8(x.clone(), scale, out_dtype)
+    got = ck.quantize_per_tensor_fp8(x.to(dev), scale.to(dev), out_dtype)
+    _fp8_equal(got, want, out_dtype)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(1000, 1000), (1024, 2048), (7, 13), (1,), (0, 5)])
 def test_quantize_fp8_random(dtype, shape, hip, dev, seed):
@@ -106,6 +141,23 @@ def test_dequantize_fp8_every_code(in_dtype, out_dtype, scale, hip, dev):
     nan = torch.isnan(w)
     assert torch.equal(nan, torch.isnan(g))
     assert torch.equal(bits(got)[~nan], bits(want)[~nan])
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float8_e4m3fn, torch.float8_e5m2], ids=["e4m3", "e5m2"])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_fp8_16bit_scale(in_dtype, scale_dtype, out_dtype, hip, dev):
+    """A f16 / bf16 scale, as eager accepts it (backends/eager/__init__.py:52-58): widened
+    exactly, then rounded to the output dtype (scale.to(out)), for every code."""
+    q = torch.arange(256, dtype=torch.int32).to(torch.uint8).repeat(40).view(in_dtype)
+    for sv in (1.0, 1.0048828125, 0.00123, 371.5, 3.1e-5, 6.0e4):
+        s = torch.tensor([sv]).to(scale_dtype)
+        want = ref.dequantize_per_tensor_fp8(q, s, out_dtype)
+        got = ck.dequantize_per_tensor_fp8(q.to(dev), s.to(dev), out_dtype)
+        assert got.dtype == out_dtype
+        nan = torch.isnan(want.float())
+        assert torch.equal(nan, torch.isnan(got.cpu().float())), sv
+        assert torch.equal(bits(got)[~nan], bits(want)[~nan]), sv
 
 
 def test_c1_full_size_round_trip(hip, dev):

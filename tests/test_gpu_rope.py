@@ -2,7 +2,10 @@
 
 Bar (north star): within 1 ULP of the output dtype for fp32 freqs.  With 16-bit
 freqs the reference computes in that 16-bit type; the kernel emulates each rounding,
-so the same 1-ULP bound is asserted there too.
+so the same 1-ULP bound is asserted there too.  fp32 x (served by eager on a GPU,
+backends/eager/__init__.py:118-131): bit-exact with 16-bit freqs; with fp32 freqs within
+2^-21 of the sum of the two product magnitudes (the kernel adds the second product with
+one rounding, eager with two).
 """
 import pytest
 import torch
@@ -102,3 +105,26 @@ def test_mismatched_q_k_shapes(hip, seed):
     wq, wk = ref.apply_rope(q, k, f)
     check(gq, wq)
     check(gk, wk)
+
+
+@pytest.mark.parametrize("freqs_dtype", [torch.float32, torch.float16, torch.bfloat16], ids=["f32", "f16", "bf16"])
+@pytest.mark.parametrize("shape", [(1, 4, 64, 128), (2, 3, 9, 6), (1, 64, 3, 64)], ids=["vec", "scalar", "bnhd"])
+def test_fp32_x(freqs_dtype, shape, hip, seed):
+    b, h, n, d = shape
+    f = torch.randn(1, 1, n, d // 2, 2, 2).to(freqs_dtype)
+    xq, xk = torch.randn(shape) * 4, torch.randn(shape)
+    wq, wk = ref.apply_rope(xq, xk, f)
+    gq, gk = ck.apply_rope(xq.cuda(), xk.cuda(), f.cuda())
+    g1 = ck.apply_rope1(xq.cuda(), f.cuda())
+    assert torch.equal(g1.cpu(), gq.cpu())
+    for g, w, x in ((gq, wq, xq), (gk, wk, xk)):
+        assert g.dtype == torch.float32 and g.shape == x.shape
+        g = g.cpu()
+        if freqs_dtype != torch.float32:
+            assert torch.equal(g, w)
+            continue
+        xp = x.double().reshape(b, h, n, d // 2, 1, 2)
+        fd = f.double()
+        mag = (fd[..., 0] * xp[..., 0]).abs() + (fd[..., 1] * xp[..., 1]).abs()
+        err = (g.double() - w.double()).reshape(mag.shape).abs()
+        assert bool((err <= mag * 2.0 ** -21 + 1e-38).all()), float((err / mag.clamp_min(1e-30)).max())
