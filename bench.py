@@ -401,23 +401,6 @@ def run_gpu(configs, steps, warmup, log):
                 res["scaled_mm_mxfp8"] = {"ms": ms, **roofline_flops(FLOPS["scaled_mm_mxfp8"], ms, FP8_PEAK_TFLOPS,
                                                                       traffic.get("scaled_mm_mxfp8"))}
                 log(f"c4 scaled_mm_mxfp8: {ms * 1e3:.1f} us")
-                # C3 -> C4 from the bf16 activation: quantize_mxfp8 + the GEMM (what the layouts
-                # run) against the GEMM that quantizes the activation in its load path
-                nset = _sets_for(2 * x.numel() + qw.numel())
-                xs = [x.clone() for _ in range(nset)]
-                chk = lambda outs: [same(o, ref) or sys.exit("graph mismatch c3->c4") for o in outs]  # noqa: E731
-                ms_fused = time_graph(lambda i: (lambda: ck.scaled_mm_mxfp8_dynamic(xs[i], qw, sw)), nset,
-                                      max(steps // 4, 5), warmup, check=chk)
-                ms_two = time_graph(lambda i: (lambda: (lambda q, s: ck.scaled_mm_mxfp8(q, qw, s, sw))(
-                    *ck.quantize_mxfp8(xs[i]))), nset, max(steps // 4, 5), warmup, check=chk)
-                del xs
-                res["scaled_mm_mxfp8_dynamic"] = {
-                    "ms": ms_fused, **roofline_flops(FLOPS["scaled_mm_mxfp8"], ms_fused, FP8_PEAK_TFLOPS),
-                    "two_call_ms": ms_two,
-                    "note": "bf16 activation [4608, 3072] quantized inside the GEMM (each of the 48 N-tiles "
-                            "quantizes its rows again) vs quantize_mxfp8 + scaled_mm_mxfp8; outputs bit-identical"}
-                log(f"c3->c4 scaled_mm_mxfp8_dynamic: {ms_fused * 1e3:.1f} us fused vs {ms_two * 1e3:.1f} us "
-                    f"quantize + GEMM")
             except RuntimeError as e:
                 res["scaled_mm_mxfp8"] = {"error": str(e)}
                 log(f"c4 scaled_mm_mxfp8 unavailable: {e}")

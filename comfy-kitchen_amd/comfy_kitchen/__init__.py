@@ -31,7 +31,6 @@ __all__ = [
     "dequantize_mxfp8",
     "scaled_mm_nvfp4",
     "scaled_mm_mxfp8",
-    "scaled_mm_mxfp8_dynamic",
     "apply_rope",
     "apply_rope1",
     "swap_nibbles",
@@ -130,18 +129,6 @@ def scaled_mm_mxfp8(a: torch.Tensor, b: torch.Tensor, block_scale_a: torch.Tenso
     """y = a @ b.T + bias on MXFP8 operands (both K-major, E8M0 block-32 scales)."""
     code = DTYPE_TO_CODE[out_dtype if out_dtype is not None else torch.bfloat16]
     return torch.ops.comfy_kitchen.scaled_mm_mxfp8(a, b, block_scale_a, block_scale_b, bias, code)
-
-
-def scaled_mm_mxfp8_dynamic(x: torch.Tensor, b: torch.Tensor, block_scale_b: torch.Tensor,
-                            bias: torch.Tensor | None = None,
-                            out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """scaled_mm_mxfp8(*quantize_mxfp8(x), b, block_scale_b) with the bf16 / f16 activation
-    quantized inside the GEMM (one launch, no codes written).  Not part of the reference's
-    API: it fuses the from_float + F.linear pair of samples/mxfp8_model_patcher.py:68-70.
-    Blocks whose E8M0 scale is 0 (amax below ~2^-118, or +-inf) contribute 0; the bias
-    must have out_dtype."""
-    code = DTYPE_TO_CODE[out_dtype if out_dtype is not None else torch.bfloat16]
-    return torch.ops.comfy_kitchen.scaled_mm_mxfp8_dynamic(x, b, block_scale_b, bias, code)
 
 
 def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,

@@ -36,7 +36,6 @@ __all__ = [
     "quantize_per_tensor_fp8",
     "scaled_mm_fp8",
     "scaled_mm_mxfp8",
-    "scaled_mm_mxfp8_dynamic",
     "scaled_mm_nvfp4",
 ]
 
@@ -62,7 +61,6 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _p, _u64]),
     "ckh_amax_scale_noalloc": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
     "ckh_quantize_nvfp4_dynamic": (_i32, [_p, _f32, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _p, _u64]),
-    "ckh_scaled_mm_mxfp8_dynamic": (_i32, [_p] * 5 + [_i64] * 3 + [_i32] * 3 + [_u64]),
 }
 ABI_VERSION = 7
 # CKH_AMAX_WORKSPACE_BYTES of include/ckh.h: the workspace ckh_amax_scale takes
@@ -320,31 +318,6 @@ def scaled_mm_mxfp8(a: torch.Tensor, b: torch.Tensor, block_scale_a: torch.Tenso
     return out
 
 
-def scaled_mm_mxfp8_dynamic(x: torch.Tensor, b: torch.Tensor, block_scale_b: torch.Tensor,
-                            bias: torch.Tensor | None = None,
-                            out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """scaled_mm_mxfp8(quantize_mxfp8(x), b) in one kernel: the bf16 / f16 activation x is
-    quantized to MXFP8 in the GEMM's load path.  The bias must have the output dtype."""
-    out_dtype = out_dtype or torch.bfloat16
-    x, b = x.contiguous(), b.contiguous()
-    m, k = x.shape
-    n, kb = b.shape
-    if k != kb:
-        raise ValueError(f"scaled_mm_mxfp8_dynamic: K mismatch {k} vs {kb}")
-    sb = block_scale_b.contiguous().view(torch.uint8)
-    need = roundup(n, 128) * roundup(k // 32, 4)
-    if sb.numel() < need:
-        raise ValueError(f"scaled_mm_mxfp8_dynamic: block_scale_b has {sb.numel()} bytes, needs {need}")
-    bias_t, bias_code = _bias_args(bias, n, x.device)
-    if bias_t is not None and bias_t.dtype != out_dtype:
-        raise ValueError(f"scaled_mm_mxfp8_dynamic: bias dtype {bias_t.dtype} must equal out_dtype {out_dtype}")
-    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
-    with _on_device(x):
-        _call("ckh_scaled_mm_mxfp8_dynamic", x.data_ptr(), b.data_ptr(), sb.data_ptr(), _ptr(bias_t),
-              out.data_ptr(), m, n, k, DTYPE_TO_CODE[x.dtype], DTYPE_TO_CODE[out_dtype], bias_code, _stream(x))
-    return out
-
-
 def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
                   bias: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     out_dtype = out_dtype or torch.bfloat16
@@ -470,12 +443,6 @@ def _build_constraints() -> dict:
                               block_scale_b=ParamConstraint(dtypes=frozenset({torch.float8_e8m0fnu})),
                               bias=ParamConstraint(dtypes=floats),
                               out_dtype=ParamConstraint(dtypes=floats)),
-        "scaled_mm_mxfp8_dynamic": fc(x=ParamConstraint(dtypes=half, shape_rules=two_d + (DivisibleBy(1, 32),)),
-                                      b=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
-                                                        shape_rules=two_d + (DivisibleBy(1, 32),)),
-                                      block_scale_b=ParamConstraint(dtypes=frozenset({torch.float8_e8m0fnu})),
-                                      bias=ParamConstraint(dtypes=floats),
-                                      out_dtype=ParamConstraint(dtypes=floats)),
         "scaled_mm_fp8": fc(a=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),
                                               shape_rules=two_d + (DivisibleBy(1, 16),)),
                             b=ParamConstraint(dtypes=frozenset({torch.float8_e4m3fn}),

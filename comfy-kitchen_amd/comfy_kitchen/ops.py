@@ -167,18 +167,6 @@ def _(a, b, block_scale_a, block_scale_b, bias, output_dtype_code):
     return torch.empty((a.shape[0], b.shape[0]), dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code], device=a.device)
 
 
-@torch.library.custom_op("comfy_kitchen::scaled_mm_mxfp8_dynamic", mutates_args=())
-def scaled_mm_mxfp8_dynamic(x: torch.Tensor, b: torch.Tensor, block_scale_b: torch.Tensor,
-                            bias: torch.Tensor | None, output_dtype_code: int) -> torch.Tensor:
-    return _dispatch("scaled_mm_mxfp8_dynamic", x=x, b=b, block_scale_b=block_scale_b, bias=bias,
-                     out_dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code])
-
-
-@scaled_mm_mxfp8_dynamic.register_fake
-def _(x, b, block_scale_b, bias, output_dtype_code):
-    return torch.empty((x.shape[0], b.shape[0]), dtype=DTYPE_CODE_TO_DTYPE[output_dtype_code], device=x.device)
-
-
 @torch.library.custom_op("comfy_kitchen::scaled_mm_fp8", mutates_args=())
 def scaled_mm_fp8(a: torch.Tensor, b: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
                   bias: torch.Tensor | None, output_dtype_code: int) -> torch.Tensor:

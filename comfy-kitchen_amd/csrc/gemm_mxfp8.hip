@@ -50,7 +50,6 @@
 #include <utility>
 
 #include "ckh_common.h"
-#include "quant_math.h"
 
 namespace ckh {
 namespace mx {
@@ -187,78 +186,6 @@ __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], u
     store_pair(L, x, tx, ty, std::make_integer_sequence<int, NP>{});
 }
 
-// 16-bit activation, quantized to MXFP8 in the load path (scaled_mm_mxfp8_dynamic): one
-// stage at a time, 64 elements = 128 bytes of each of the tile's 256 rows.  Wave w, load j
-// covers rows R = 64 w + 8 j .. +7: lane i fetches 16-byte chunk c = i % 8 (8 elements)
-// of row R + i / 8, so each 8 lanes read one whole 128-byte line and lanes 4b .. 4b+3 of
-// a row hold its 32-element block b.  The chunk's 8 E4M3 codes go to logical chunk c / 2,
-// half c % 2, of the row in the stage's activation tile (physical chunk (c/2) ^ swz(row)).
-struct Loader16 {
-    __amdgpu_buffer_rsrc_t rs;
-    uint32_t voff;      // lane's global byte offset for j = 0, stage 0
-    uint32_t rowstep;   // 8 rows: global distance between consecutive loads j
-    uint32_t lds_even;  // LDS offset of the codes within a stage tile for even j (adds 512 j);
-                        // for odd j the chunk index is xor 1, i.e. the offset xor 16
-    uint32_t sc_off;    // offset of the row's scale word in the stage buffer's activation
-                        // scale area (j = 0), plus the block's byte within the stage
-};
-
-__device__ __forceinline__ Loader16 make_loader16(const uint8_t* tile_base, int valid_rows, int K, int wave,
-                                                  int lane) {
-    Loader16 L;
-    L.rs = buffer_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * 2u * K);
-    const int row = 64 * wave + (lane >> 3), c = lane & 7;
-    L.voff = static_cast<uint32_t>(row * 2 * K + 16 * c);
-    L.rowstep = 16u * K;
-    L.lds_even = static_cast<uint32_t>(row * BK + ((((c >> 1) ^ swz(row))) << 4) + (c & 1) * 8);
-    // word of row R = 64 w + 8 j + i/8 in a 256-row scale chunk pair: (R/128)*512 +
-    // (R%32)*16 + ((R%128)/32)*4, and block b = c/4 of the stage's two is byte b of the
-    // stage's pair of bytes
-    L.sc_off = static_cast<uint32_t>((wave >> 1) * 512 + (lane >> 3) * 16 + (wave & 1) * 8 + (c >> 2));
-    return L;
-}
-
-// Offset added for stage s: past K the lane reads zeros from outside the descriptor.
-__device__ __forceinline__ uint32_t stage_add16(int k0, int K, int lane) {
-    return (k0 + 8 * (lane & 7) < K) ? static_cast<uint32_t>(2 * k0) : 0x80000000u;
-}
-
-template <int J>
-__device__ __forceinline__ void load_piece16(const Loader16& L, v4u (&x)[8], uint32_t add) {
-    x[J] = __builtin_amdgcn_raw_buffer_load_b128(L.rs, L.voff + J * L.rowstep + add, 0, 0);
-}
-
-// Quantize piece J (8 elements of one 32-element block) as quantize_mxfp8 does (the codes
-// and exponent of mx_codes16 but for scale-0 blocks, below; block amax over the lane quad)
-// and store its codes to the stage tile at
-// `tile`; the quad stores the block's E8M0 byte to the stage's scale area `sc` at byte
-// 2 * ODD + b of the row's word, the byte the stage's MFMAs select.
-template <int AIN, int J, bool ODD>
-__device__ __forceinline__ void quantize_piece16(const Loader16& L, const v4u (&x)[8], uint8_t* tile, uint8_t* sc,
-                                                 int lane) {
-    const uint4 w = make_uint4(x[J][0], x[J][1], x[J][2], x[J][3]);
-    uint32_t m = amax16x8(w);
-    m = max(m, dpp<0xB1>(m));  // quad_perm [1,0,3,2]
-    m = max(m, dpp<0x4E>(m));  // quad_perm [2,3,0,1]
-    const uint32_t bits = amax16_to_f32_bits<AIN>(m);
-    // Branch-free (a branch here splits the stage's hand-scheduled slots and lets the
-    // compiler sink the MFMAs past the stage barriers).  Exponent 0 is a zero block (+0
-    // codes, as quantize_mxfp8) or a scale of 0.0 (infinite amax, or a nonzero amax of at
-    // most ~1.3e-36), where quantize_mxfp8 writes 0x7E|sign / 0xFF codes whose products
-    // with scale byte 0 are +-448 * 2^-127 * b: here such a block contributes 0, or NaN
-    // codes when it holds a NaN (amax NaN), so the output keeps the NaN.
-    const uint32_t e = mx_exponent_select(bits);
-    const float scale = as_f((e ? e : 1u) << 23);
-    uint2 codes = make_uint2(scaled_e4m3x4<AIN>(w.x, w.y, scale), scaled_e4m3x4<AIN>(w.z, w.w, scale));
-    // materialised here: otherwise the compiler sinks the converts into a branch on e
-    __asm__ volatile("" : "+v"(codes.x), "+v"(codes.y));
-    const uint32_t fill = bits > 0x7f800000u ? ~0u : 0u;
-    codes = e ? codes : make_uint2(fill, fill);
-    *reinterpret_cast<uint2*>(tile + ((J & 1) ? (L.lds_even ^ 16u) : L.lds_even) + 512 * J) = codes;
-    // all four lanes of the quad store the same byte (a guard would be a branch)
-    sc[L.sc_off + (J & 3) * 128 + (J >> 2) * 4 + (ODD ? 2 : 0)] = static_cast<uint8_t>(e);
-}
-
 // Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
 // two contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
 // (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand w >> 1 (0 = weight,
@@ -371,20 +298,12 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 // 256 x 128 half tiles that finish a grid whose last round would leave most CUs idle.
 // bid: the workgroup's index among the workgroups of its kind (full or half tiles).
 //
-// AIN: -1 when the activation is E4M3 codes with E8M0 scales; CKH_BF16 / CKH_F16 when it
-// is a 16-bit tensor quantized to MXFP8 in the load path (scaled_mm_mxfp8_dynamic): each
-// stage t quantizes the activation of stage t + 2 into its buffer (codes and the E8M0
-// bytes its MFMAs select) and loads that of stage t + 3, so the activation moves one stage
-// at a time through the same 32 staging registers; every wave moves weight scale words.
-//
 // Stage buffers 0, 1 and 2, 3 live in two arrays.  Every stage reads fragments from one
 // array and writes staged data into the other, so the compiler knows they never alias
 // and may interleave the two freely; within an array, per-lane addresses of different
 // buffers differ only by immediates.
-template <int OUT, int BIAS, bool UNIT, int NW, int AIN>
+template <int OUT, int BIAS, bool UNIT, int NW>
 __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01, uint8_t* lds23) {
-    constexpr bool AQ = AIN >= 0;
-    static_assert(!(AQ && UNIT), "the in-load quantize produces block scales");
     constexpr int TBN = 64 * NW;  // tile width along n
     constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
     constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
@@ -407,11 +326,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
 
     const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * p.K, min(TBN, p.N - n0), p.K, wave, lane, TBN / 4);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * p.K, min(BM, p.M - m0), p.K, wave, lane);
-    const Loader16 LA16 = make_loader16(p.a + static_cast<int64_t>(m0) * 2 * p.K, min(BM, p.M - m0), p.K, wave, lane);
-    // scale words: waves 0, 1 move the weight's, waves 2, 3 the activation's; with the
-    // in-load quantize, waves 2, 3 repeat waves 0, 1 (identical bytes to the same LDS
-    // words: a branch instead would let the compiler sink the MFMAs past the barriers)
-    const int swave = AQ ? (wave & 1) : wave;
+    // scale words: waves 0, 1 move the weight's, waves 2, 3 the activation's
     const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
@@ -434,20 +349,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     ScaleWords SW;
     auto load_b = [&](int s) {
         load_pair<PB>(LB, SB, s * BK, p.K);
-        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, swave, lane);
-    };
-    // the activation of stage s into x (16-bit path)
-    auto load_a16 = [&](v4u (&x)[8], int s) {
-        const uint32_t add = stage_add16(s * BK, p.K, lane);
-        for_each_index([&](auto j_c) { load_piece16<decltype(j_c)::value>(LA16, x, add); },
-                       std::make_integer_sequence<int, 8>{});
-    };
-    // quantize the staged activation x of stage s (parity ODD) into buffer b_c
-    auto quantize_a16 = [&](const v4u (&x)[8], auto b_c, auto odd_c) {
-        for_each_index([&](auto j_c) {
-            quantize_piece16<AIN, decltype(j_c)::value, decltype(odd_c)::value>(LA16, x, buf(b_c) + TILE,
-                                                                                buf(b_c) + 2 * TILE + STILE, lane);
-        }, std::make_integer_sequence<int, 8>{});
+        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
@@ -502,7 +404,6 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         uint8_t* wx = EVEN ? buf(P2{}) : buf(P3{}) + TILE;
         uint8_t* wy = EVEN ? buf(P3{}) : buf(b_c) + TILE;
         const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, p.K) : pair_add(LB, (t + 3) * BK, p.K);
-        const uint32_t add16 = stage_add16((t + 3) * BK, p.K, lane);
         v4u wb, wa;
         uint32_t nb[4], na[4];
         auto slot = [&](auto k_c) {
@@ -517,14 +418,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
             if constexpr (k == 1) G.a[0] = read_frag(nx + TILE, faa);
             if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
             if constexpr (k % 4 == 3 && k / 4 < NW) FB[k / 4] = read_frag(nx + (k / 4) * 32 * BK, fab);
-            if constexpr (k < 8 && AQ) {
-                quantize_piece16<AIN, k, !EVEN>(LA16, SA, buf(P2{}) + TILE, buf(P2{}) + 2 * TILE + STILE, lane);
-                load_piece16<k>(LA16, SA, add16);
-                if constexpr (k < PB) {
-                    if constexpr (EVEN) store_piece<k>(LB, SB, wx, wy);
-                    else load_piece<k>(LB, SB, add);
-                }
-            } else if constexpr (k < 8) {
+            if constexpr (k < 8) {
                 if constexpr (EVEN) {
                     if constexpr (k < PB) store_piece<k>(LB, SB, wx, wy);
                     load_piece<k>(LA, SA, add);
@@ -534,8 +428,8 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
                 }
             }
             if constexpr (k == (SLOTS > 8 ? 8 : SLOTS - 1) && !UNIT) {
-                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, swave, lane);
-                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, swave, lane);
+                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
+                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
             }
             if constexpr (k == SLOTS - 4) {
 #pragma unroll
@@ -562,22 +456,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // prologue: stages 0..3 resident except the weight half of 2, 3 (staged in SB for
     // stage 0 to write), stage 0 read.  All four pairs are loaded before the first LDS
     // write, so the prologue waits out one memory latency rather than two.
-    if constexpr (AQ) {
-        // activation stages 0, 1 quantized into their buffers, stage 2 staged in SA for
-        // stage 0 to quantize; weight as below
-        v4u XA[8], X1[8], XB[8];
-        ScaleWords XW;
-        load_a16(XA, 0);
-        load_a16(X1, 1);
-        load_pair<PB>(LB, XB, 0, p.K);
-        load_scales(XW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, 0, p.K, swave, lane);
-        load_b(2);
-        load_a16(SA, 2);
-        quantize_a16(XA, B0{}, std::false_type{});
-        quantize_a16(X1, B1{}, std::true_type{});
-        store_pair<PB>(LB, XB, buf(B0{}), buf(B1{}));
-        store_scales(XW, buf(B0{}) + 2 * TILE, buf(B1{}) + 2 * TILE, swave, lane);
-    } else {
+    {
         v4u XA[8], XB[8];
         ScaleWords XW;
         load_a(0);
@@ -690,16 +569,282 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
 // The dispatcher starts half-tile workgroups on CUs as their last full tile ends, so
 // the tail overlaps the uneven end of the previous round instead of waiting for a
 // second launch.
-template <int OUT, int BIAS, bool UNIT, int AIN>
+template <int OUT, int BIAS, bool UNIT>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
     const int b = blockIdx.x;
-    if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4, AIN>(p, b, lds01, lds23);
-    else gemm_tile<OUT, BIAS, UNIT, 2, AIN>(p, b - p.n_full, lds01, lds23);
+    if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4>(p, b, lds01, lds23);
+    else gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
 }
 
 }  // namespace mx
+
+// ------------------------------------------------------------ skinny activations
+// GEMMs with few activation rows (M <= 64: batch-size-1 modulation and projection linears)
+// read every weight byte once and do little arithmetic per byte, so they are bound by HBM
+// bandwidth on the weight, not by the matrix cores.  The 256 x 256 tiles above would give
+// such a GEMM only N / 256 workgroups.  Here a workgroup owns 32 or 64 weight rows and all of
+// K (N / 32 = 576 workgroups for N = 18432, several resident per CU), and its waves split
+// the K steps in chunks of 4 (256 bytes of each row), chunk c to wave c % WV.  A wave stages
+// its chunk of weight rows (and, for M <= 16, of activation rows) in its own LDS area with
+// direct-to-LDS loads in which every instruction reads 8 whole 128-byte lines, then reads
+// its MFMA fragments from there: loading the fragments straight from memory asks for 32-byte
+// pieces of 32 lines per instruction and measured 18.9 against 15.1 us at M = 1,
+// N = 18432, K = 3072.  The weight loads are nontemporal; the activation, read by every
+// workgroup, stays cached.  At the end the K partials meet in LDS and each wave adds and
+// stores its share of the tile.  Operand layout and scale selection are the tile kernel's
+// (lane l = 32 h + r: row r, bytes k0 + 16 h and k0 + 32 + 16 h; scale word shifted by
+// 8 h, opsel 0 / 2 for even / odd steps of a 128-wide scale block).  Rows past M or N and
+// bytes past K lie outside the buffer descriptors and load as zeros.
+namespace sk {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kSkChunk = 4;              // K steps (64 bytes) per wave per chunk: two scale words
+constexpr int kSkRow = 64 * kSkChunk;    // staged bytes per row and chunk (256)
+constexpr int kSkCpr = kSkRow / 16;      // 16-byte chunks per staged row
+constexpr int kSkRpl = 1024 / kSkRow;    // staged rows per direct-to-LDS load (1 KB)
+constexpr int kAuxNontemporal = 2;       // buffer-load cache policy bit: the weight is read once
+
+struct Args {
+    const uint8_t* a;
+    const uint8_t* b;
+    const uint8_t* sa;
+    const uint8_t* sb;
+    const void* bias;
+    void* out;
+    int M, N, K;
+    int ncb;               // scale column blocks: ceil(K/32/4)
+    int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
+    const float* tsa;      // per-tensor mode: the two fp32 tensor scales (device)
+    const float* tsb;
+};
+
+// Staging layout: row r of a chunk is 256 bytes; logical 16-byte chunk c sits at physical
+// chunk c ^ (r % 16).  LDS banks repeat every 256 bytes, so a fragment read (16 lanes = 16
+// consecutive rows, one logical chunk) hits 16 distinct 16-byte bank groups.
+__device__ __forceinline__ uint32_t sk_swz(int r) { return static_cast<uint32_t>(r & (kSkCpr - 1)); }
+
+// Direct-to-LDS whole-line loads of rows [0, NQ * kSkRpl) of a chunk: load q writes 1 KB,
+// rows kSkRpl q .. , lane i to row kSkRpl q + i / kSkCpr, physical chunk i % kSkCpr, so each
+// load reads 8 whole 128-byte lines.  Bytes past K, and rows outside the descriptor, arrive
+// as zeros.
+template <int NQ, int AUX>
+__device__ __forceinline__ void stage_rows(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int K, int kbase, int lane) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int row = kSkRpl * q + lane / kSkCpr;
+        const int k = kbase + static_cast<int>(((lane % kSkCpr) ^ sk_swz(row)) << 4);
+        const uint32_t off = k < K ? static_cast<uint32_t>(row * K + k) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + q * 1024), 16, off, 0, 0, AUX);
+    }
+}
+
+// This lane's MFMA operand for step j of the staged chunk: row r, logical chunks 4 j + h and
+// 4 j + 2 + h (bytes k0 + 16 h and k0 + 32 + 16 h of the step).
+__device__ __forceinline__ v8i staged_frag(const uint8_t* st, int r, int h, int j) {
+    const uint8_t* row = st + r * kSkRow;
+    const uint32_t s = sk_swz(r);
+    const v4u x = *reinterpret_cast<const v4u*>(row + (((4 * j + h) ^ s) << 4));
+    const v4u y = *reinterpret_cast<const v4u*>(row + (((4 * j + 2 + h) ^ s) << 4));
+    return v8i{(int)x[0], (int)x[1], (int)x[2], (int)x[3], (int)y[0], (int)y[1], (int)y[2], (int)y[3]};
+}
+
+// Offset of this lane's piece p (0, 1) of the step at k0 for a direct (unstaged) operand
+// load: bytes k0 + 32 p + 16 h of its row; past K it reads zeros.
+__device__ __forceinline__ uint32_t piece_off(uint32_t row_off, int k0, int p, int h, int K) {
+    const int k = k0 + 32 * p + 16 * h;
+    return k < K ? row_off + static_cast<uint32_t>(k) : 0x80000000u;
+}
+
+// One chunk's register-held operands: scale words and (unstaged activation) fragments.
+template <int MT, int NT>
+struct SkRegs {
+    uint32_t swb[NT][kSkChunk / 2], swa[MT][kSkChunk / 2];
+    v4u al[MT][kSkChunk][2];
+};
+
+// WV: waves per workgroup, each taking every WV-th K chunk.
+// NT: 32-row weight tiles per workgroup (1 or 2); each activation fragment feeds NT MFMAs.
+// MT: 32-row activation tiles (M <= 32 MT).
+// AR: activation rows staged through LDS like the weight (8 or 16, >= M, one M-tile), or 0:
+// the activation's fragments are loaded straight into registers.
+template <int OUT, int BIAS, bool UNIT, int WV, int NT, int MT, int AR>
+__global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
+    static_assert(AR == 0 || (MT == 1 && AR % kSkRpl == 0 && AR <= 32), "staged activation: one tile");
+    static_assert(16 % WV == 0, "each wave stores 16 / WV accumulator registers");
+    constexpr int WR = 32 * NT;                   // weight rows of the workgroup
+    constexpr int WST = (WR + AR) * kSkRow;       // staged bytes per wave
+    constexpr int RED = WV * NT * MT * 16 * 64 * 4;
+    constexpr int LDS = WV * WST > RED ? WV * WST : RED;
+    __shared__ __attribute__((aligned(1024))) uint8_t stage[LDS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5, r = lane & 31;
+    // row group of this workgroup: the groups are dealt so that each XCD (blockIdx % 8) runs a
+    // contiguous range of them, so the 32-row groups that share a 128-row block of swizzled
+    // scale lines run on one XCD (its L2 fetches those lines once)
+    int grp = blockIdx.x;
+    if ((gridDim.x & 7) == 0) grp = (grp & 7) * (gridDim.x >> 3) + (grp >> 3);
+    const int n0 = grp * WR;
+
+    const __amdgpu_buffer_rsrc_t rb =
+        buffer_rsrc(p.b + static_cast<int64_t>(n0) * p.K, static_cast<uint32_t>(min(WR, p.N - n0)) * p.K);
+    __amdgpu_buffer_rsrc_t ra[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        ra[t] = buffer_rsrc(p.a + static_cast<int64_t>(32 * t) * p.K,
+                            static_cast<uint32_t>(max(0, min(32, p.M - 32 * t))) * p.K);
+    // per-tensor mode: no scale tensors (zero-sized descriptors, never loaded)
+    const __amdgpu_buffer_rsrc_t rsb = buffer_rsrc(p.sb, UNIT ? 0u : static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rsa = buffer_rsrc(p.sa, UNIT ? 0u : static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
+    const uint32_t row_off = static_cast<uint32_t>(r * p.K);
+    // scale word of row r (of the 32-row group) in column block cb: swizzled offset
+    // ((row/128 * ncb + cb) * 32 + row%32) * 16 + ((row%128)/32) * 4
+    uint32_t sb_row[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int nu = n0 + 32 * u;
+        sb_row[u] = static_cast<uint32_t>((nu >> 7) * p.ncb * 512 + r * 16 + ((nu & 127) >> 5) * 4);
+    }
+    const uint32_t sa_row = static_cast<uint32_t>(r * 16);  // activation rows 32 t + r: + 4 t
+    const int KT = (p.K + 63) / 64;
+    const int NC = (KT + kSkChunk - 1) / kSkChunk;
+
+    // issue chunk c's loads: weight (and staged activation) rows to LDS buffer `buf`, scale
+    // words and unstaged activation fragments to R
+    uint8_t* stb = stage + wave * WST;  // this wave's staged rows: weight, then activation
+    auto issue = [&](int c, SkRegs<MT, NT>& R) {
+        const int s0 = c * kSkChunk;
+        // the weight is read once (nontemporal); the activation, which every workgroup
+        // reads, stays cached
+        stage_rows<WR / kSkRpl, kAuxNontemporal>(rb, stb, p.K, s0 * 64, lane);
+        if constexpr (AR > 0) stage_rows<AR / kSkRpl, 0>(ra[0], stb + WR * kSkRow, p.K, s0 * 64, lane);
+        if constexpr (!UNIT) {
+#pragma unroll
+            for (int u = 0; u < kSkChunk / 2; ++u) {
+                const int cb = (s0 >> 1) + u;  // 128-wide scale block of steps s0 + 2u, s0 + 2u + 1
+                const uint32_t cbo = cb < p.ncb ? static_cast<uint32_t>(cb * 512) : 0x80000000u;
+#pragma unroll
+                for (int v = 0; v < NT; ++v)
+                    R.swb[v][u] = __builtin_amdgcn_raw_buffer_load_b32(rsb, sb_row[v] + cbo, 0, 0);
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    R.swa[t][u] = __builtin_amdgcn_raw_buffer_load_b32(rsa, sa_row + t * 4 + cbo, 0, 0);
+            }
+        }
+        if constexpr (AR == 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int j = 0; j < kSkChunk; ++j)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                        R.al[t][j][q] = __builtin_amdgcn_raw_buffer_load_b128(
+                            ra[t], piece_off(row_off, (s0 + j) * 64, q, h, p.K), 0, 0);
+        }
+    };
+
+    v16f acc[NT][MT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[u][t] = v16f{};
+
+    // this wave's chunks: c = wave, wave + WV, ...; the staged rows are the wave's own, so
+    // waiting for its own loads is enough (no barrier)
+    SkRegs<MT, NT> cur;
+    if (wave < NC) issue(wave, cur);
+    for (int c = wave; c < NC; c += WV) {
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(mx::waitcnt_vm_lgkm0(0));
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < kSkChunk; ++j) {
+            v8i fa[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                if constexpr (AR > 0) {
+                    fa[t] = staged_frag(stb + WR * kSkRow, r < AR ? r : 0, h, j);
+                    if (r >= AR) fa[t] = v8i{};
+                } else {
+                    const v4u u = cur.al[t][j][0], w = cur.al[t][j][1];
+                    fa[t] = v8i{(int)u[0], (int)u[1], (int)u[2], (int)u[3], (int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NT; ++u) {
+                const v8i fb = staged_frag(stb + u * 32 * kSkRow, r, h, j);
+                const uint32_t sbv = UNIT ? 0x7f7f7f7fu : cur.swb[u][j >> 1] >> (8 * h);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const uint32_t sav = UNIT ? 0x7f7f7f7fu : cur.swa[t][j >> 1] >> (8 * h);
+                    if (j & 1)
+                        acc[u][t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb, fa[t], acc[u][t], 0, 0, 2, sbv, 2, sav);
+                    else
+                        acc[u][t] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb, fa[t], acc[u][t], 0, 0, 0, sbv, 0, sav);
+                }
+            }
+        }
+        // the next chunk's loads overwrite the staged rows: every fragment read is done
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(mx::waitcnt_vm_lgkm0(63));
+        __asm__ volatile("" ::: "memory");
+        if (c + WV < NC) issue(c + WV, cur);
+    }
+
+    // the K partials of each 32 x 32 tile meet in LDS (reusing the staging area); wave w adds
+    // and stores registers RPW w .. RPW w + RPW - 1 (columns n0 + 32 u + 8 (v / 4) + 4 h + v % 4
+    // of row m = 32 t + r)
+    constexpr int RPW = 16 / WV;
+    __syncthreads();
+    float (*red)[NT][MT][16][64] = reinterpret_cast<float (*)[NT][MT][16][64]>(stage);
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[wave][u][t][v][lane] = acc[u][t][v];
+    __syncthreads();
+    const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
+    const int v0 = RPW * wave;
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int n = n0 + 32 * u + 8 * (v0 >> 2) + 4 * h + (v0 & 3);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int m = 32 * t + r;
+            float v[RPW];
+#pragma unroll
+            for (int e = 0; e < RPW; ++e) {
+                float s = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WV; ++w) s += red[w][u][t][v0 + e][lane];
+                if constexpr (UNIT) s *= alpha;
+                if constexpr (BIAS >= 0) s += n + e < p.N ? load1<BIAS>(p.bias, n + e) : 0.0f;
+                // kept from being fused with the narrowing into one mixed-precision rounding
+                v[e] = (UNIT || BIAS >= 0) ? opaque(s) : s;
+            }
+            if (m >= p.M) continue;
+            const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+            if constexpr (RPW == 4) {
+                if (n + 3 < p.N && (p.N & 3) == 0) {
+                    mx::store4<OUT>(p.out, idx, v);
+                    continue;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < RPW; ++e)
+                if (n + e < p.N) mx::store1<OUT>(p.out, idx + e, v[e]);
+        }
+    }
+}
+
+}  // namespace sk
 }  // namespace ckh
 
 using namespace ckh;
@@ -709,15 +854,12 @@ namespace {
 // Workgroups that can hold a 256 x 256 tile at once: one per CU.
 constexpr int kGemmSlots = 256;
 
-// The 16-bit-activation kernels take a bias of the output's dtype only (as the layouts
-// pass it), which keeps their instantiations to three per activation dtype.
-template <bool UNIT, int AIN>
+template <bool UNIT>
 void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT, AIN>), dim3(wgs), dim3(mx::NT), 0, st, p)
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_kernel<O, B, UNIT>), dim3(wgs), dim3(mx::NT), 0, st, p)
 #define BY_BIAS(O)                                                     \
     do {                                                               \
         if (!has_bias) LAUNCH(O, -1);                                  \
-        else if constexpr (AIN >= 0) LAUNCH(O, O);                     \
         else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32);             \
         else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16);             \
         else LAUNCH(O, CKH_BF16);                                      \
@@ -729,17 +871,56 @@ void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, b
 #undef LAUNCH
 }
 
+// Activations of at most kSkinnyMaxM rows take the skinny kernel (sk::gemm_skinny_kernel).
+constexpr int kSkinnyMaxM = 64;
+
+template <bool UNIT>
+int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    sk::Args p{};
+    p.a = q.a; p.b = q.b; p.sa = q.sa; p.sb = q.sb; p.bias = q.bias; p.out = q.out;
+    p.M = q.M; p.N = q.N; p.K = q.K; p.ncb = q.ncb; p.sa_rows = q.sa_rows; p.sb_rows = q.sb_rows;
+    p.tsa = q.tsa; p.tsb = q.tsb;
+    // per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
+    // staged activation rows (measured on N = 18432, K = 3072: M = 1 12.7 us, M = 16 15.4 us,
+    // M = 32 20.5 us, M = 64 26.4 us)
+#define LAUNCH(O, B, WV, NT, MT, AR)                                                              \
+    hipLaunchKernelGGL((sk::gemm_skinny_kernel<O, B, UNIT, WV, NT, MT, AR>),                      \
+                       dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
+#define BY_MT(O, B)                                    \
+    do {                                               \
+        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);        \
+        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16); \
+        else if (p.M <= 32) LAUNCH(O, B, 4, 2, 1, 0);  \
+        else LAUNCH(O, B, 4, 2, 2, 0);                 \
+    } while (0)
+#define BY_BIAS(O)                                          \
+    do {                                                    \
+        if (!has_bias) BY_MT(O, -1);                        \
+        else if (bias_code == CKH_F32) BY_MT(O, CKH_F32);   \
+        else if (bias_code == CKH_F16) BY_MT(O, CKH_F16);   \
+        else BY_MT(O, CKH_BF16);                            \
+    } while (0)
+    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+    else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef BY_MT
+#undef LAUNCH
+    return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
+}
+
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
 // half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
 // half tiles (about 55% of a full tile's time each), in the same grid.
-template <bool UNIT, int AIN = -1>
+template <bool UNIT>
 int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    if (p.M <= kSkinnyMaxM) return launch_skinny<UNIT>(p, out_code, bias_code, has_bias, st);
     const int tiles = p.tiles_m * p.tiles_n;
     const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : 0;
     p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
     p.n_full = tiles - p.n_half;
-    launch_grid<UNIT, AIN>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
-    return check_launch(UNIT ? "scaled_mm_fp8" : AIN >= 0 ? "scaled_mm_mxfp8_dynamic" : "scaled_mm_mxfp8");
+    launch_grid<UNIT>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
+    return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }
 
 mx::Args base_args(const void* a, const void* b, const void* bias, void* out, int64_t M, int64_t N, int64_t K) {
@@ -801,32 +982,4 @@ extern "C" int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scal
     p.tsa = scale_a;
     p.tsb = scale_b;
     return launch_gemm<true>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
-}
-
-extern "C" int ckh_scaled_mm_mxfp8_dynamic(const void* a, const void* b, const void* sb, const void* bias, void* out,
-                                           int64_t M, int64_t N, int64_t K, int a_code, int out_code, int bias_code,
-                                           uintptr_t stream) {
-    CKH_REQUIRE(a && b && sb && out, "scaled_mm_mxfp8_dynamic: null pointer");
-    CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_mxfp8_dynamic: sizes must be M, N >= 0 and K > 0");
-    CKH_REQUIRE(K % 32 == 0, "scaled_mm_mxfp8_dynamic: K (%lld) must be a multiple of 32", (long long)K);
-    CKH_REQUIRE(a_code == CKH_BF16 || a_code == CKH_F16,
-                "scaled_mm_mxfp8_dynamic: unsupported activation dtype code %d (bf16 or f16)", a_code);
-    CKH_REQUIRE(2 * M * K < (1ll << 31) && N * K < (1ll << 31) && K < (1ll << 24),
-                "scaled_mm_mxfp8_dynamic: operand larger than 2 GiB");
-    CKH_REQUIRE(out_code == CKH_F32 || out_code == CKH_F16 || out_code == CKH_BF16,
-                "scaled_mm_mxfp8_dynamic: unsupported output dtype code %d", out_code);
-    CKH_REQUIRE(!bias || bias_code == out_code,
-                "scaled_mm_mxfp8_dynamic: bias dtype code %d must be the output's (%d)", bias_code, out_code);
-    CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sb, 4) && aligned(out, 16),
-                "scaled_mm_mxfp8_dynamic: pointers misaligned");
-    if (M == 0 || N == 0) return CKH_OK;
-    mx::Args p = base_args(a, b, bias, out, M, N, K);
-    p.sa = static_cast<const uint8_t*>(sb);  // unused: the activation's scales are made in the kernel
-    p.sb = static_cast<const uint8_t*>(sb);
-    p.ncb = static_cast<int>(cdiv(K / 32, 4));
-    p.sa_rows = 0;
-    p.sb_rows = static_cast<int>(rup(N, 128));
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (a_code == CKH_BF16) return launch_gemm<false, CKH_BF16>(p, out_code, bias_code, bias != nullptr, st);
-    return launch_gemm<false, CKH_F16>(p, out_code, bias_code, bias != nullptr, st);
 }

@@ -112,9 +112,7 @@ __device__ __forceinline__ void unpack16x8(uint4 w, float (&v)[8]) {
 
 // Codes of one lane's 8 packed 16-bit values w (E4M3) and the E8M0 exponent e of their
 // 32-element block, whose amax has fp32 bits `bits`: the packed scaled convert on the
-// common range, the general encoder for zero, tiny and non-finite blocks.  This is the
-// MXFP8 quantizer's step; the bf16-activation GEMM calls it too, so both produce the same
-// codes and scales.
+// common range, the general encoder for zero, tiny and non-finite blocks.
 template <int IN>
 __device__ __forceinline__ uint2 mx_codes16(uint4 w, uint32_t bits, uint32_t& e) {
     if (bits >= (10u << 23) && bits < 0x7f800000u) {
@@ -126,19 +124,6 @@ __device__ __forceinline__ uint2 mx_codes16(uint4 w, uint32_t bits, uint32_t& e)
     float v[8];
     unpack16x8<IN>(w, v);
     return mx_encode8(v, bits, e);
-}
-
-// mx_exponent without branches (the same value for every input): the closed form on the
-// common range, 0 for non-finite amax, and for amax below 2^-117 (biased exponent < 10)
-// two thresholds: the division form s = RN(amax / 448) gives e = 0 up to amax bits
-// 0x04600001 (s <= 2^-127), 1 up to 0x04E00000 (s <= 2^-126) and 2 above (s < 2^-125),
-// found by evaluating it on every such amax.
-__device__ __forceinline__ uint32_t mx_exponent_select(uint32_t bits) {
-    uint32_t fast = (bits >> 23) - 8u + ((bits & 0x7fffffu) > 0x600000u);
-    uint32_t tiny = (bits > 0x04600001u ? 1u : 0u) + (bits > 0x04e00000u ? 1u : 0u);
-    // both materialised, so the compiler keeps the selects (no branch on the range)
-    __asm__ volatile("" : "+v"(fast), "+v"(tiny));
-    return bits >= 0x7f800000u ? 0u : (bits >= (10u << 23) ? fast : tiny);
 }
 
 // Pack 8 non-NaN values into E2M1 nibbles with the hardware convert: RNE, identical to

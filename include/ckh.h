@@ -152,27 +152,6 @@ int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa, const void
                         int out_code, int bias_code, uintptr_t stream);
 
 /*
- * MXFP8 GEMM on a bf16 / f16 activation: a [M,K] of a_code (bf16 or f16, row-major) is
- * quantized to E4M3 codes and E8M0 block-32 scales inside the GEMM's load path (nothing
- * is written back), then multiplied as ckh_scaled_mm_mxfp8 does with b [N,K] e4m3 and its
- * swizzled scales sb.  For every block whose E8M0 scale is nonzero, and for all-zero
- * blocks, the codes and scale equal ckh_quantize_mxfp8's, so the output equals
- * ckh_quantize_mxfp8 + ckh_scaled_mm_mxfp8 bit for bit.  Blocks whose scale byte is 0
- * (amax below about 2^-118, or +-inf) contribute 0 where the two-call path has
- * +-448 * 2^-127 * b terms (NaN if such an inf block also holds a 0); blocks holding a
- * NaN give NaN.  bias NULL or [N] of out_code; out [M,N] of out_code (f32/f16/bf16).
- * K % 32 == 0; a, b and out 16-byte aligned.  Each 256-column N-tile quantizes its
- * activation rows again (N/256 times in all): on the Flux up-projection [4608, 12288, 3072]
- * that takes about twice the time of the two calls, so the layouts keep the two calls.
- * No counterpart in the reference, which quantizes the activation with
- * QuantizedTensor.from_float and then calls F.linear (samples/mxfp8_model_patcher.py:61-70,
- * tensor/mxfp8.py:54-74); this replaces that pair of calls.
- */
-int ckh_scaled_mm_mxfp8_dynamic(const void* a, const void* b, const void* sb, const void* bias,
-                                void* out, int64_t M, int64_t N, int64_t K, int a_code,
-                                int out_code, int bias_code, uintptr_t stream);
-
-/*
  * Per-tensor FP8 GEMM: out[M,N] = scale_a * scale_b * sum_k A[m,k] * B[n,k] (+ bias[n]).
  * a [M,K] e4m3, b [N,K] e4m3 (both K-major), scale_a / scale_b one f32 each on device;
  * bias NULL or [N] of bias_code; out [M,N] row-major of out_code.  K % 16 == 0.

@@ -177,14 +177,6 @@ __device__ bool sweep_nvfp4_decode(uint64_t i) {
     return ok;
 }
 
-// 13: mx_exponent_select (the bf16-activation GEMM's branch-free exponent) == mx_exponent
-// for every 32-bit amax pattern.
-__device__ bool sweep_mx_exponent_select(uint64_t i) {
-    const uint32_t a = static_cast<uint32_t>(i);
-    if (a & 0x80000000u) return true;  // an amax is non-negative
-    return mx_exponent_select(a) == mx_exponent(a);
-}
-
 template <int S>
 __device__ bool check(uint64_t i) {
     if constexpr (S == 0) return sweep_e4m3(i);
@@ -199,8 +191,7 @@ __device__ bool check(uint64_t i) {
     else if constexpr (S == 9) return sweep_markstein<CKH_F16>(i);
     else if constexpr (S == 10) return sweep_c_steps(i);
     else if constexpr (S == 11) return sweep_mx_exponent(i);
-    else if constexpr (S == 12) return sweep_nvfp4_decode(i);
-    else return sweep_mx_exponent_select(i);
+    else return sweep_nvfp4_decode(i);
 }
 
 template <int S>
@@ -221,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void sweep_kernel(uint64_t begin, uint64_
 // Domain size (number of indices) of sweep `which`, or 0 for an unknown sweep.
 extern "C" uint64_t ckh_hw_sweep_size(int which) {
     switch (which) {
-        case 0: case 1: case 2: case 3: case 11: case 13: return uint64_t(1) << 32;
+        case 0: case 1: case 2: case 3: case 11: return uint64_t(1) << 32;
         case 4: return 256;
         case 5: case 6: return (uint64_t(1) << 16) * 254;
         case 7: return uint64_t(198u - 57u) << 23;
@@ -256,7 +247,6 @@ extern "C" int ckh_hw_sweep(int which, uint64_t begin, uint64_t end, void* count
         case 10: L(10); break;
         case 11: L(11); break;
         case 12: L(12); break;
-        case 13: L(13); break;
         default: return 1;
     }
 #undef L

@@ -89,17 +89,3 @@ def test_quantize_nvfp4_dynamic_rejects_bad_arguments(lib):
     assert b"empty tensor" in lib.ckh_last_error()
     assert f(p, 2688.0, p, p, p, 16, 40, 16, 40, 0.0, 2, 1, p, 0) == 1
     assert b"multiple of 16" in lib.ckh_last_error()
-
-
-def test_scaled_mm_mxfp8_dynamic_rejects_bad_arguments(lib):
-    buf = ctypes.create_string_buffer(256)
-    p = ctypes.addressof(buf)
-    f = lib.ckh_scaled_mm_mxfp8_dynamic
-    assert f(None, p, p, None, p, 64, 64, 64, 2, 2, 0, 0) == 1
-    assert b"null pointer" in lib.ckh_last_error()
-    assert f(p, p, p, None, p, 64, 64, 48, 2, 2, 0, 0) == 1
-    assert b"multiple of 32" in lib.ckh_last_error()
-    assert f(p, p, p, None, p, 64, 64, 64, 0, 2, 0, 0) == 1  # f32 activation
-    assert b"activation dtype" in lib.ckh_last_error()
-    assert f(p, p, p, p, p, 64, 64, 64, 2, 2, 0, 0) == 1  # f32 bias, bf16 output
-    assert b"must be the output's" in lib.ckh_last_error()

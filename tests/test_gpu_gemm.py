@@ -108,91 +108,46 @@ def test_scaled_mm_mxfp8_config4_full(hip):
     assert rel_l2(got[rows], want_cpu) <= 4e-3
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 3072), (8, 200, 288), (9, 64, 1024), (16, 1000, 3072), (17, 1000, 3072),
+                                   (31, 96, 224), (32, 4096, 64), (33, 130, 5120), (40, 33, 96), (64, 512, 1056),
+                                   (2, 33, 32), (48, 18432, 128)])
+def test_scaled_mm_mxfp8_skinny(m, n, k, out_dtype, hip):
+    """At most 64 activation rows take the skinny kernel (a workgroup per 32 or 64 weight
+    rows, K split over its waves; four configurations by M, boundaries 8 / 16 / 32 / 64):
+    rows past M, columns past N, K % 64 == 32, K past one chunk round and long K."""
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=m * 13 + n + k)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("m", [1, 12, 20, 40])
+def test_scaled_mm_skinny_bias_and_per_tensor(bias_dtype, m, hip):
+    """The skinny kernel's epilogue: bias of each dtype, and the per-tensor FP8 mode
+    (ck.scaled_mm_fp8: unit block scales, out = scale_a * scale_b * A B^T + bias)."""
+    n, k = 300, 640
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=m + 77)
+    bias = (torch.randn(n) * 2).to(bias_dtype)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), bias=bias.cuda(), out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+    ta, tb = torch.tensor([0.37]), torch.tensor([1.9e-3])
+    want = (qx.float() @ qw.float().t()) * (ta * tb) + bias.float()
+    for out_dtype in (torch.float32, torch.bfloat16):
+        got = ck.scaled_mm_fp8(qx.cuda(), qw.cuda(), ta.cuda(), tb.cuda(), bias=bias.cuda(), out_dtype=out_dtype)
+        assert got.shape == (m, n) and got.dtype == out_dtype
+        assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
 def test_scaled_mm_mxfp8_rejects_bad_shapes(hip):
     a = torch.zeros(64, 96, dtype=torch.float8_e4m3fn, device="cuda")
     b = torch.zeros(64, 64, dtype=torch.float8_e4m3fn, device="cuda")
     s = torch.zeros(128, 4, dtype=torch.float8_e8m0fnu, device="cuda")
     with pytest.raises((ValueError, RuntimeError)):
         ck.scaled_mm_mxfp8(a, b, s, s)
-
-
-# ---------------------------------------------- MXFP8 GEMM on a bf16 / f16 activation
-def _two_call(x, qw, sw, bias, out_dtype):
-    qx, sx = ck.quantize_mxfp8(x)
-    return ck.scaled_mm_mxfp8(qx, qw, sx, sw, bias=bias, out_dtype=out_dtype)
-
-
-@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.bfloat16, True),
-                                                 (torch.float16, True), (torch.float32, False)])
-@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (300, 500, 160), (33, 17, 96), (1, 64, 32),
-                                   (512, 1024, 3072), (4352, 4196, 128)])
-def test_scaled_mm_mxfp8_dynamic_equals_quantize_then_gemm(m, n, k, x_dtype, out_dtype, with_bias, hip):
-    """Quantizing in the GEMM's load path gives the codes and scales quantize_mxfp8 writes,
-    so the output equals quantize_mxfp8 + scaled_mm_mxfp8 bit for bit (same MFMA order);
-    against the CPU oracle it meets the GEMM bar.  (4352, 4196) runs the half-width tail tiles."""
-    g = torch.Generator().manual_seed(m + 3 * n + k)
-    x = (torch.randn(m, k, generator=g) * torch.exp(torch.randn(m, 1, generator=g))).to(x_dtype)
-    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
-    bias = (torch.randn(n, generator=g) * 2).to(out_dtype) if with_bias else None
-    qw, sw = ck.quantize_mxfp8(w.cuda())
-    xd, bd = x.cuda(), (None if bias is None else bias.cuda())
-    got = ck.scaled_mm_mxfp8_dynamic(xd, qw, sw, bias=bd, out_dtype=out_dtype)
-    assert got.shape == (m, n) and got.dtype == out_dtype
-    assert torch.equal(got, _two_call(xd, qw, sw, bd, out_dtype))
-    if m * n * k <= 1 << 28:
-        qx, sx = ref.quantize_mxfp8(x)
-        want = ref.scaled_mm_mxfp8_ref(qx, qw.cpu(), sx, sw.cpu(), bias=bias, out_dtype=torch.float32)
-        assert rel_l2(got, want) <= REL_L2[out_dtype]
-
-
-def test_scaled_mm_mxfp8_dynamic_special_blocks(hip):
-    """Zero, NaN, inf and tiny blocks.  A block whose E8M0 scale byte is 0 (amax below
-    ~2^-118, or +-inf) contributes 0: the output equals the two-call path on x with those
-    blocks zeroed, bit for bit.  A NaN anywhere in a row makes the row NaN in both paths."""
-    m, n, k = 160, 320, 256
-    g = torch.Generator().manual_seed(77)
-    x = torch.randn(m, k, generator=g).bfloat16()
-    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
-    x[0] = 0                              # zero row: output is the bias
-    x[1, :32] = 0                         # zero block
-    x[2, 5] = float("nan")                # NaN block
-    x[3, 32:64] = 1e-37 * torch.sign(x[3, 32:64])  # tiny block: E8M0 scale 0
-    x[4, 64:96] = 1.0
-    x[4, 70] = float("-inf")              # inf block without zeros
-    x[5, 96:128] = 0
-    x[5, 100] = float("inf")              # inf block holding zeros (the two-call path gives NaN)
-    x[6, 128:160] = 3e-36                 # tiny block just above the scale-0 threshold (E8M0 byte 1)
-    x[7, 160:192] = 1e-30                 # small block with a normal scale
-    bias = torch.randn(n, generator=g).bfloat16().cuda()
-    qw, sw = ck.quantize_mxfp8(w.cuda())
-    xd = x.cuda()
-    got = ck.scaled_mm_mxfp8_dynamic(xd, qw, sw, bias=bias)
-    two = _two_call(xd, qw, sw, bias, torch.bfloat16)
-    nan_rows = torch.zeros(m, dtype=torch.bool)
-    nan_rows[2] = True
-    assert got[2].isnan().all() and two[2].isnan().all()
-    assert two[5].isnan().all() and not got[5].isnan().any()
-    _, sx = ck.quantize_mxfp8(xd)
-    scale0 = ref.from_blocked(sx.cpu().view(torch.uint8), m, k // 32) == 0       # [m, k/32]
-    assert scale0[3, 1] and scale0[4, 2] and scale0[5, 3] and not scale0[6, 4] and not scale0[7, 5]
-    zeroed = x.clone().view(m, k // 32, 32)
-    zeroed[scale0 & ~x.view(m, k // 32, 32).isnan().any(-1)] = 0
-    want = _two_call(zeroed.view(m, k).cuda(), qw, sw, bias, torch.bfloat16)
-    assert torch.equal(got[~nan_rows], want[~nan_rows])
-    assert torch.equal(got[0], bias)
-    for r in (1, 3, 4, 6, 7):             # rows without NaN agree with the two calls to the bar
-        assert rel_l2(got[r:r + 1], two[r:r + 1]) <= 4e-3
-
-
-def test_scaled_mm_mxfp8_dynamic_rejects_bad_arguments(hip):
-    x = torch.zeros(64, 96, dtype=torch.bfloat16, device="cuda")
-    b = torch.zeros(64, 96, dtype=torch.float8_e4m3fn, device="cuda")
-    s = torch.zeros(128, 4, dtype=torch.float8_e8m0fnu, device="cuda")
-    with pytest.raises((ValueError, RuntimeError), match="bias dtype"):
-        ck.scaled_mm_mxfp8_dynamic(x, b, s, bias=torch.zeros(64, device="cuda"))
-    with pytest.raises((ValueError, RuntimeError)):
-        ck.scaled_mm_mxfp8_dynamic(x[:, :80], b[:, :80], s)
 
 
 # --------------------------------------------------------------------- NVFP4

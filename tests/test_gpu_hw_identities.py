@@ -12,7 +12,6 @@ software or IEEE definitions over each identity's whole domain:
   Markstein quotient codes      every T significand x every bf16 / f16 v (both signs)
   (amax/6)/g Markstein steps    every f16 amax significand x every g significand
   MXFP8 exponent closed form    every finite amax with biased exponent >= 10
-  branch-free MXFP8 exponent    every 32-bit amax pattern
   NVFP4 GEMM operand decode     every code byte x every pair of finite scale bytes
 
 A toolchain or ROCm change that broke one of them would break the quantizers' or the
@@ -31,7 +30,6 @@ SWEEPS = {
     "e4m3_convert": 0, "e5m2_convert": 1, "bf16_convert": 2, "e2m1_pack": 3, "e4m3_decode": 4,
     "scaled_e4m3_bf16": 5, "scaled_e4m3_f16": 6, "rcp_newton": 7, "markstein_bf16": 8,
     "markstein_f16": 9, "nvfp4_scale_steps": 10, "mx_exponent": 11, "nvfp4_gemm_decode": 12,
-    "mx_exponent_select": 13,
 }
 CHUNK = 1 << 34  # indices per launch (each launch well under a second)
 
