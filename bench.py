@@ -266,20 +266,43 @@ def copy_floor_calls(read_bytes: int, write_bytes: int):
     return make, nset
 
 
-def time_with_floor(name: str, make_call, n_sets: int, steps: int, warmup: int, check=None) -> tuple[float, float]:
-    """(ms per call of the op, ms per call of the copy floor for its bytes): both graphs
-    captured, then timed in alternating rounds (time_replays)."""
+def vendor_copy_calls(nbytes: int):
+    """(make_call, n_sets) of torch's own device copy (Tensor.copy_ on uint8 tensors) of
+    nbytes, reading and writing nbytes each, over buffer sets rotating through > 512 MB."""
+    dev = torch.device("cuda", 0)
+    nset = _sets_for(2 * nbytes)
+    srcs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(nset)]
+    dsts = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(nset)]
+
+    def make(i):
+        def call():
+            return dsts[i].copy_(srcs[i])
+        return call
+
+    return make, nset
+
+
+def time_with_floor(name: str, make_call, n_sets: int, steps: int, warmup: int, check=None) -> tuple[float, dict]:
+    """(ms per call of the op, {"ours": ms of the copy floor for its bytes, "vendor": ms of
+    torch's device copy moving the same total bytes}): the three graphs captured, then timed
+    in alternating rounds (time_replays)."""
     g_op = capture_graph(make_call, n_sets, steps, warmup, check)
-    fmake, fn = copy_floor_calls(*READ_WRITE[name])
+    rd, wr = READ_WRITE[name]
+    fmake, fn = copy_floor_calls(rd, wr)
     g_floor = capture_graph(fmake, fn, steps, warmup)
-    ms, floor = time_replays([g_op, g_floor], steps)
-    return ms, floor
+    vmake, vn = vendor_copy_calls((rd + wr) // 2)
+    g_vendor = capture_graph(vmake, vn, steps, warmup)
+    ms, floor, vendor = time_replays([g_op, g_floor, g_vendor], steps)
+    return ms, {"ours": floor, "vendor": vendor}
 
 
-def record_floor(res: dict, name: str, floor: float, log) -> None:
-    res[name]["copy_floor_ms"] = floor
-    res[name]["of_copy_floor"] = round(floor / res[name]["ms"], 4)
-    log(f"   copy floor for {name}'s bytes: {floor * 1e3:.2f} us ({res[name]['of_copy_floor'] * 100:.1f}% of it)")
+def record_floor(res: dict, name: str, floor: dict, log) -> None:
+    res[name]["copy_floor_ms"] = floor["ours"]
+    res[name]["of_copy_floor"] = round(floor["ours"] / res[name]["ms"], 4)
+    res[name]["vendor_copy_ms"] = floor["vendor"]
+    res[name]["of_vendor_copy"] = round(floor["vendor"] / res[name]["ms"], 4)
+    log(f"   copy floor for {name}'s bytes: {floor['ours'] * 1e3:.2f} us ({res[name]['of_copy_floor'] * 100:.1f}% of "
+        f"it); torch copy_ of the same bytes: {floor['vendor'] * 1e3:.2f} us ({res[name]['of_vendor_copy'] * 100:.1f}%)")
 
 
 def roofline_bytes(nbytes, ms, traffic=None):
@@ -305,6 +328,146 @@ def load_traffic() -> dict:
         except (ValueError, OSError, AttributeError):
             return {}
     return {}
+
+
+# ------------------------------------------------------------------ GEMMs
+# Flux / Wan-14B linear shapes (M, N, K) the reference's model patchers quantize
+# (samples/mxfp8_model_patcher.py:78-117 patches every nn.Linear): Flux double-block qkv,
+# projection, MLP up / down at 4608 image tokens; the modulation linears at batch 1 and 16;
+# Wan-14B attention and FFN at 8192 tokens.
+LINEAR_SHAPES = [
+    ("flux_qkv", 4608, 9216, 3072), ("flux_proj", 4608, 3072, 3072), ("flux_mlp_up", 4608, 12288, 3072),
+    ("flux_mlp_down", 4608, 3072, 12288), ("flux_mod_m1", 1, 18432, 3072), ("flux_mod_m16", 16, 18432, 3072),
+    ("wan_attn", 8192, 5120, 5120), ("wan_ffn_up", 8192, 13824, 5120), ("wan_ffn_down", 8192, 5120, 13824),
+]
+
+
+def gemm_operands(m: int, n: int, k: int, seed: int, dev):
+    """MXFP8 operands of a linear: activation N(0, 1), weight N(0, 0.02), both bf16 quantized
+    by ck.quantize_mxfp8 (seeded, generated on the device)."""
+    import comfy_kitchen as ck
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(m, k, device=dev, generator=g).bfloat16()
+    w = (torch.randn(n, k, device=dev, generator=g) * 0.02).bfloat16()
+    qa, sa = ck.quantize_mxfp8(x)
+    qw, sw = ck.quantize_mxfp8(w)
+    return qa, sa, qw, sw
+
+
+def time_gemm_variants(qa, sa, qw, sw, steps: int, warmup: int, vendor: bool = True) -> dict:
+    """ms per call of ck.scaled_mm_mxfp8 ("mx"), ck.scaled_mm_fp8 with unit tensor scales
+    ("fp8"), and the vendor GEMMs the reference calls on a GPU: torch._scaled_mm tensor-wise
+    ("vendor_fp8", TensorCoreFP8Layout's F.scaled_mm path) and torch's F.scaled_mm with 1 x 32
+    E8M0 scales ("vendor_mx", eager scaled_mm_mxfp8), each a HIP graph over rotating operand
+    sets.  The vendor MX GEMM reads row-major (unswizzled) scales: with the reference's
+    SWIZZLE_32_4_4 argument on these swizzled scales, torch on ROCm returns wrong results,
+    whose rel-L2 against ours is recorded as "vendor_mx_reference_call_rel_l2"."""
+    import torch.nn.functional as F
+
+    import comfy_kitchen as ck
+
+    m, k = qa.shape
+    n = qw.shape[0]
+    nset = _sets_for(qa.numel() + qw.numel())
+    sets = [(qa.clone(), qw.clone(), sa.clone(), sw.clone()) for _ in range(nset)]
+    one = torch.ones(1, device=qa.device)
+    k_steps = max(steps // 2, 10)
+    out = {}
+    ref = ck.scaled_mm_mxfp8(qa, qw, sa, sw)
+
+    def same(outs):
+        for o in outs:
+            if not torch.equal(o, ref):
+                sys.exit("graph replay mismatch in a GEMM")
+
+    cands = [("mx", lambda i: (lambda: ck.scaled_mm_mxfp8(*sets[i])), same),
+             ("fp8", lambda i: (lambda: ck.scaled_mm_fp8(sets[i][0], sets[i][1], one, one)), None)]
+    if vendor:
+        one0 = one.reshape(())
+        cands.append(("vendor_fp8", lambda i: (lambda: torch._scaled_mm(sets[i][0], sets[i][1].t(), one0, one0,
+                                                                        out_dtype=torch.bfloat16)), None))
+        try:
+            sa_p = ck.from_blocked(sa.view(torch.uint8), m, k // 32).contiguous().view(torch.float8_e8m0fnu)
+            sw_p = ck.from_blocked(sw.view(torch.uint8), n, k // 32).contiguous().view(torch.float8_e8m0fnu)
+
+            def vmx(a, b, x, y, swz):
+                return F.scaled_mm(a, b.t(), scale_a=x, scale_recipe_a=F.ScalingType.BlockWise1x32, scale_b=y,
+                                   scale_recipe_b=F.ScalingType.BlockWise1x32, swizzle_a=swz, swizzle_b=swz,
+                                   output_dtype=torch.bfloat16)
+            rel = lambda o: round(float((o.float() - ref.float()).norm() / ref.float().norm()), 5)  # noqa: E731
+            out["vendor_mx_rel_l2"] = rel(vmx(qa, qw, sa_p, sw_p, F.SwizzleType.NO_SWIZZLE))
+            out["vendor_mx_reference_call_rel_l2"] = rel(vmx(qa, qw, sa, sw, F.SwizzleType.SWIZZLE_32_4_4))
+            cands.append(("vendor_mx", lambda i: (lambda: vmx(sets[i][0], sets[i][1], sa_p, sw_p,
+                                                              F.SwizzleType.NO_SWIZZLE)), None))
+        except (RuntimeError, ValueError) as e:
+            out["vendor_mx_error"] = str(e)[:200]
+    graphs, names = [], []
+    for name, make, chk in cands:
+        try:
+            graphs.append(capture_graph(make, nset, k_steps, warmup, chk))
+            names.append(name)
+        except (RuntimeError, ValueError) as e:
+            out[f"{name}_error"] = str(e)[:200]
+    for name, ms in zip(names, time_replays(graphs, k_steps)):
+        out[f"{name}_ms"] = ms
+    del sets, graphs
+    return out
+
+
+def run_linear_shapes(steps: int, warmup: int, log) -> dict:
+    """ops.linear_shapes: each LINEAR_SHAPES entry's GEMM times (time_gemm_variants), TFLOPS
+    and fraction of the dense FP8 peak; for M <= 256 also the weight bytes (codes + scales)
+    per second and their fraction of HBM peak."""
+    dev = torch.device("cuda", 0)
+    res = {}
+    for i, (name, m, n, k) in enumerate(LINEAR_SHAPES):
+        qa, sa, qw, sw = gemm_operands(m, n, k, 100 + i, dev)
+        t = time_gemm_variants(qa, sa, qw, sw, steps, warmup)
+        flops = 2 * m * n * k
+        e = {"M": m, "N": n, "K": k}
+        for key in ("mx", "fp8", "vendor_fp8", "vendor_mx"):
+            if f"{key}_ms" in t:
+                ms = t[f"{key}_ms"]
+                e[key] = {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                          "frac_fp8_peak": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+                if m <= 256:
+                    wb = qw.numel() + sw.numel()
+                    gbs = wb / (ms * 1e-3) / 1e9
+                    e[key].update({"weight_gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        e.update({k2: v for k2, v in t.items() if not k2.endswith("_ms")})
+        res[name] = e
+        log(f"linear {name} [{m}, {n}, {k}]: " + ", ".join(
+            f"{key} {e[key]['ms'] * 1e3:.1f} us" for key in ("mx", "fp8", "vendor_fp8", "vendor_mx") if key in e))
+        del qa, sa, qw, sw
+    return res
+
+
+def run_copy_sweep(log) -> dict:
+    """The two copies (benchlib/copy_floor.hip and torch's Tensor.copy_), each moving S bytes
+    (S/2 read + S/2 written) for S from 32 MB to 1 GB, graph-timed over rotating buffers, and
+    a least-squares fit t = fixed + S / rate per copy: the fixed per-call cost and the
+    asymptotic rate that bound a streaming kernel of a given size."""
+    sizes = [32 << 20, 64 << 20, 128 << 20, 256 << 20, 512 << 20, 1024 << 20]
+    out = {"bytes_moved": sizes, "ours_us": [], "vendor_us": []}
+    for sz in sizes:
+        fmake, fn = copy_floor_calls(sz // 2, sz // 2)
+        vmake, vn = vendor_copy_calls(sz // 2)
+        steps = 20
+        g1 = capture_graph(fmake, fn, steps, 3)
+        g2 = capture_graph(vmake, vn, steps, 3)
+        a, b = time_replays([g1, g2], steps)
+        out["ours_us"].append(round(a * 1e3, 2))
+        out["vendor_us"].append(round(b * 1e3, 2))
+        del g1, g2
+    for key in ("ours", "vendor"):
+        ts = out[f"{key}_us"]
+        n = len(sizes)
+        mx_, my = sum(sizes) / n, sum(ts) / n
+        slope = sum((x - mx_) * (y - my) for x, y in zip(sizes, ts)) / sum((x - mx_) ** 2 for x in sizes)
+        out[f"{key}_fit"] = {"fixed_us": round(my - slope * mx_, 2), "rate_gbs": round(1e-3 / slope, 1)}
+    log(f"copy sweep: ours {out['ours_fit']}, torch copy_ {out['vendor_fit']}")
+    return out
 
 
 # ------------------------------------------------------------------ runs
@@ -401,6 +564,20 @@ def run_gpu(configs, steps, warmup, log):
                 res["scaled_mm_mxfp8"] = {"ms": ms, **roofline_flops(FLOPS["scaled_mm_mxfp8"], ms, FP8_PEAK_TFLOPS,
                                                                       traffic.get("scaled_mm_mxfp8"))}
                 log(f"c4 scaled_mm_mxfp8: {ms * 1e3:.1f} us")
+                # the same shape through ck.scaled_mm_fp8 and the vendor GEMMs, in one set of
+                # alternating rounds
+                t = time_gemm_variants(qa, sa, qw, sw, steps, warmup)
+                for key, name in (("mx", "scaled_mm_mxfp8_same_run"), ("fp8", "scaled_mm_fp8"),
+                                  ("vendor_fp8", "scaled_mm_fp8_vendor"), ("vendor_mx", "scaled_mm_mxfp8_vendor")):
+                    if f"{key}_ms" in t:
+                        res[name] = {"ms": t[f"{key}_ms"], **roofline_flops(FLOPS["scaled_mm_mxfp8"], t[f"{key}_ms"],
+                                                                         FP8_PEAK_TFLOPS)}
+                res["scaled_mm_mxfp8_vendor"] = {**res.get("scaled_mm_mxfp8_vendor", {}),
+                                                 **{k2: v for k2, v in t.items() if k2.startswith("vendor_mx_")},
+                                                 "what": "torch F.scaled_mm, BlockWise1x32 E8M0, row-major scales"}
+                res["scaled_mm_fp8_vendor"] = {**res.get("scaled_mm_fp8_vendor", {}),
+                                               "what": "torch._scaled_mm tensor-wise FP8 (C4 codes, unit scales)"}
+                log("c4 same run: " + ", ".join(f"{k2} {v * 1e3:.1f} us" for k2, v in t.items() if k2.endswith("_ms")))
             except RuntimeError as e:
                 res["scaled_mm_mxfp8"] = {"error": str(e)}
                 log(f"c4 scaled_mm_mxfp8 unavailable: {e}")
@@ -467,17 +644,29 @@ def run_gpu(configs, steps, warmup, log):
 
 
 def host_info() -> dict:
-    """CPU model, logical CPU count and torch version of this host."""
-    model = ""
+    """CPU model (the model-name string plus family / model / stepping, since a virtualised
+    host may shorten the name), logical CPU count, torch's CPU vector capability (it sets the
+    eager kernels' vector width) and torch version of this host."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model", "stepping", "vendor_id") and key not in info:
+                    info[key] = val.strip()
+                if not line.strip() and info:
                     break
     except OSError:
         pass
-    return {"cpu_model": model, "host_cpus": os.cpu_count(), "torch": torch.__version__}
+    try:
+        cap = torch.backends.cpu.get_cpu_capability()
+    except (AttributeError, RuntimeError):
+        cap = ""
+    model = info.get("model name", "")
+    ident = ", ".join(f"{k} {info[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in info)
+    return {"cpu_model": f"{model} ({ident})" if ident else model, "host_cpus": os.cpu_count(),
+            "torch_cpu_capability": cap, "torch": torch.__version__}
 
 
 def run_cpu_baseline(configs, log):
@@ -741,7 +930,7 @@ PROFILE_OPS = {
     "apply_rope1": ("c2", "rope_wave_kernel<2, 0, true>"),
     "quantize_mxfp8": ("c3", "quantize_mxfp8_fast_kernel<2>"),
     "dequantize_mxfp8": ("c3", "dequantize_mxfp8_fast_kernel<2>"),
-    "scaled_mm_mxfp8": ("c4", "mx::gemm_kernel<2, -1, false, -1>"),
+    "scaled_mm_mxfp8": ("c4", "mx::gemm_kernel<2, -1, false>"),
     "quantize_nvfp4": ("c5", "quantize_nvfp4_fast_kernel<2, true, 16, false>"),
     "dequantize_nvfp4": ("c5", "dequantize_nvfp4_tile_kernel<2, true>"),
     "scaled_mm_nvfp4": ("c5", "nv::gemm_kernel<2, -1>"),
@@ -828,6 +1017,133 @@ def summarize_trace(kt_dir: str, bench_json: str, command: str):
               f"bench {us:.2f} us)")
 
 
+# C4 GEMMs side by side with the vendor's: `--pmc-gemm-driver` dispatches the MFMA-loop
+# calibration, the 256 MiB traffic calibration, then PMC_CALLS calls each of
+# ck.scaled_mm_mxfp8, ck.scaled_mm_fp8 (unit scales), torch._scaled_mm tensor-wise and
+# torch's F.scaled_mm with 1 x 32 E8M0 scales on the C4 operands; `--summarize-gemm` joins a
+# kernel-trace run, an SQ-counter run and a FETCH_SIZE run of it into
+# profiles/scaled_mm_c4_vs_vendor.md.
+GEMM_OPS = ("ck.scaled_mm_mxfp8", "ck.scaled_mm_fp8", "torch._scaled_mm tensor-wise",
+            "F.scaled_mm BlockWise1x32 (row-major E8M0)")
+
+
+def pmc_gemm_driver():
+    import torch.nn.functional as F
+
+    import comfy_kitchen as ck
+
+    dev = torch.device("cuda", 0)
+    qa, sa = ck.quantize_mxfp8(make_c3(dev))
+    qw, sw = ck.quantize_mxfp8(make_c4_weight(dev))
+    m, k = qa.shape
+    n = qw.shape[0]
+    one = torch.ones(1, device=dev)
+    sa_p = ck.from_blocked(sa.view(torch.uint8), m, k // 32).contiguous().view(torch.float8_e8m0fnu)
+    sw_p = ck.from_blocked(sw.view(torch.uint8), n, k // 32).contiguous().view(torch.float8_e8m0fnu)
+    calls = [lambda: ck.scaled_mm_mxfp8(qa, qw, sa, sw), lambda: ck.scaled_mm_fp8(qa, qw, one, one),
+             lambda: torch._scaled_mm(qa, qw.t(), one.reshape(()), one.reshape(()), out_dtype=torch.bfloat16),
+             # the swizzle arguments must be given: torch 2.10 on ROCm dereferences a null
+             # pointer on the host when they are left out
+             lambda: F.scaled_mm(qa, qw.t(), scale_a=sa_p, scale_recipe_a=F.ScalingType.BlockWise1x32, scale_b=sw_p,
+                                 scale_recipe_b=F.ScalingType.BlockWise1x32, swizzle_a=F.SwizzleType.NO_SWIZZLE,
+                                 swizzle_b=F.SwizzleType.NO_SWIZZLE, output_dtype=torch.bfloat16)]
+    for c in calls:  # warm up outside the counted sequence order (the summary matches by name)
+        c()
+    src = torch.ones(PMC_CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(cus * 256, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    assert bench_lib().ckh_bench_mfma_loop(sink.data_ptr(), cus, PMC_MFMA_ITERS,
+                                           torch.cuda.current_stream().cuda_stream) == 0
+    torch.neg(src, out=dst)
+    for c in calls:
+        for _ in range(PMC_CALLS):
+            c()
+    torch.cuda.synchronize()
+    print(json.dumps({"gemm_sequence": GEMM_OPS, "calls": PMC_CALLS}), flush=True)
+
+
+def summarize_gemm(kt_dir: str, sq_dir: str, fetch_dir: str, command: str):
+    """profiles/scaled_mm_c4_vs_vendor.md (+ .json): per GEMM kernel of the --pmc-gemm-driver
+    sequence, its duration (kernel trace), the clock its SQ_BUSY_CYCLES imply over that
+    duration, MFMA busy, instruction mix, LDS conflicts and L2-miss fetch bytes."""
+    import csv
+    import statistics
+
+    def rows(d, fname):
+        out = []
+        for f in sorted(Path(d).rglob(fname)):
+            with open(f) as fh:
+                out += list(csv.DictReader(fh))
+        return out
+
+    kt = sorted(rows(kt_dir, "*kernel_trace.csv"), key=lambda r: int(r["Start_Timestamp"]))
+    dur = {}
+    for r in kt:
+        dur.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+
+    def per_dispatch(d):
+        disp = {}
+        for r in rows(d, "*counter_collection.csv"):
+            e = disp.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], {}])
+            e[1][r["Counter_Name"]] = e[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        return [disp[i] for i in sorted(disp)]
+
+    sq, fe = per_dispatch(sq_dir), per_dispatch(fetch_dir)
+    cal = next(c for name, c in sq if "mfma_loop_kernel" in name)
+    cal_name = next(name for name, _ in sq if "mfma_loop_kernel" in name)
+    full = cal["SQ_VALU_MFMA_BUSY_CYCLES"] / cal["SQ_BUSY_CYCLES"]
+    # the calibration loop: PMC_MFMA_ITERS x 16 MFMAs of 64 cycles per wave, all SIMDs busy
+    cal_cycles = PMC_MFMA_ITERS * 16 * 64
+    n_se = cal["SQ_BUSY_CYCLES"] / cal_cycles
+    cal_us = statistics.median(dur.get(cal_name, [float("nan")]))
+    fcal = max((c["FETCH_SIZE"], name) for name, c in fe if "mfma_loop" not in name and "ckh::" not in name
+               and "gemm" not in name.lower() and "Cijk" not in name)
+    fscale = PMC_CALIB_BYTES / (fcal[0] * 1024.0)
+    gemm = lambda name: ("ckh::" in name and "gemm" in name) or "Cijk" in name or "GEMM" in name  # noqa: E731
+    table = {}
+    for name, c in sq:
+        if gemm(name):
+            table.setdefault(name, {"sq": [], "fetch": []})["sq"].append(c)
+    for name, c in fe:
+        if name in table:
+            table[name]["fetch"].append(c["FETCH_SIZE"] * 1024.0 * fscale)
+    out = {"command": command, "calibration": {"kernel": cal_name[:60], "mfma_busy_per_sq_busy": round(full, 3),
+                                               "shader_engines": round(n_se, 2), "median_us": round(cal_us, 2),
+                                               "clock_ghz": round(cal_cycles / cal_us / 1e3, 3)},
+           "kernels": {}}
+    lines = ["# C4 GEMMs against the vendor's (hipBLASLt through torch) — counters side by side", "",
+             "Sequence (`python3 -u bench.py --pmc-gemm-driver`): the MFMA-loop calibration, a 256 MiB negate "
+             "(traffic calibration), then three calls each of " + ", ".join(f"`{o}`" for o in GEMM_OPS) +
+             " on the C4 operands (A [4608, 3072], B [12288, 3072], bf16 out).", "",
+             "Commands (each a run of its own):", "", f"    {command}", "",
+             "- implied clock = SQ_BUSY_CYCLES / shader engines / duration (shader engines from the calibration "
+             f"loop, whose MFMA cycles are known: {n_se:.2f}); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES "
+             f"÷ the calibration's ratio ({full:.3f});",
+             "- fetch = TCC FETCH_SIZE scaled by the traffic calibration: bytes that missed L2 (HBM + MALL).", "",
+             "| kernel | calls | mean µs | implied clock GHz | MFMA busy | MFMA insts | LDS insts | LDS bank-conflict "
+             "cycles | VALU insts / MFMA | fetch MB |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for name, e in table.items():
+        mean = {cn: statistics.mean(c[cn] for c in e["sq"]) for cn in e["sq"][0]}
+        us = statistics.mean(dur.get(name, [float("nan")])[-PMC_CALLS:])
+        clock = mean["SQ_BUSY_CYCLES"] / n_se / us / 1e3
+        busy = mean["SQ_VALU_MFMA_BUSY_CYCLES"] / mean["SQ_BUSY_CYCLES"] / full
+        vpm = mean["SQ_INSTS_VALU"] / mean["SQ_INSTS_MFMA"] if mean.get("SQ_INSTS_MFMA") else float("nan")
+        fetch = statistics.mean(e["fetch"]) / 1e6 if e["fetch"] else float("nan")
+        out["kernels"][name] = {"calls": len(e["sq"]), "mean_us": round(us, 2), "clock_ghz": round(clock, 3),
+                                "mfma_busy": round(busy, 4), "valu_per_mfma": round(vpm, 2),
+                                "fetch_bytes": round(fetch * 1e6), **{cn: round(v) for cn, v in sorted(mean.items())}}
+        lines.append(f"| `{name[:90]}` | {len(e['sq'])} | {us:.1f} | {clock:.2f} | {100 * busy:.1f}% | "
+                     f"{mean['SQ_INSTS_MFMA']:,.0f} | {mean['SQ_INSTS_LDS']:,.0f} | {mean['SQ_LDS_BANK_CONFLICT']:,.0f} | "
+                     f"{vpm:.2f} | {fetch:.1f} |")
+    prof = REPO / "profiles"
+    prof.mkdir(exist_ok=True)
+    (prof / "scaled_mm_c4_vs_vendor.md").write_text("\n".join(lines) + "\n")
+    (prof / "scaled_mm_c4_vs_vendor.json").write_text(json.dumps(out, indent=1) + "\n")
+    print("\n".join(lines))
+
+
 def pmc_sequence_names(configs):
     names = []
     if "c1" in configs:
@@ -848,7 +1164,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--configs", default="c1,c2,c3,c4,c5,lin,sweep",
+                    help="BASELINE configs c1..c5, lin (Flux/Wan linear shapes), sweep (copy size sweep)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--pmc-driver", action="store_true", help="dispatch sequence for rocprofv3 --pmc passes")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -856,6 +1173,10 @@ def main():
     ap.add_argument("--pmc-command", default="", help="command recorded in profiles/traffic.json")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("KT_DIR", "BENCH_JSON"),
                     help="write profiles/<op>_<config>.md from a rocprofv3 --kernel-trace run and a bench line")
+    ap.add_argument("--pmc-gemm-driver", action="store_true",
+                    help="C4 GEMM sequence (ours and the vendor's) for rocprofv3 passes")
+    ap.add_argument("--summarize-gemm", nargs=3, metavar=("KT_DIR", "SQ_DIR", "FETCH_DIR"),
+                    help="write profiles/scaled_mm_c4_vs_vendor.md from runs of --pmc-gemm-driver")
     ap.add_argument("--summarize-counters", metavar="SQ_DIR",
                     help="write profiles/counters.json (MFMA busy, LDS conflicts) from a rocprofv3 --pmc pass "
                          "over SQ_COUNTERS")
@@ -868,6 +1189,9 @@ def main():
         return
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace, args.pmc_command)
+        return
+    if args.summarize_gemm:
+        summarize_gemm(*args.summarize_gemm, args.pmc_command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -887,7 +1211,13 @@ def main():
     if args.pmc_driver:
         pmc_driver(configs)
         return
+    if args.pmc_gemm_driver:
+        pmc_gemm_driver()
+        return
     gpu = run_gpu(configs, args.steps, args.warmup, log)
+    if "lin" in configs:
+        gpu["linear_shapes"] = run_linear_shapes(args.steps, args.warmup, log)
+    sweep = run_copy_sweep(log) if "sweep" in configs else None
     cpu = {} if args.no_cpu else run_cpu_baseline(configs, log)
 
     primary = "quantize_mxfp8" if "quantize_mxfp8" in gpu else next(iter(gpu))
@@ -913,6 +1243,7 @@ def main():
         "cpu_baseline": cpu.get(primary),
         "ops": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()} for k, v in gpu.items()},
         "cpu_baselines": cpu,
+        "copy_sweep": sweep,
         "device": torch.cuda.get_device_properties(0).gcnArchName,
     }
     print(json.dumps(line), flush=True)

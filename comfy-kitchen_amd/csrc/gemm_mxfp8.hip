@@ -21,11 +21,13 @@
 // descriptors' ranges and load as zeros, so every stage runs the same branch-free code.
 //
 // Pipeline: at stage t (after its barrier) the fragments of t are already in
-// registers; the LDS reads of stage t+1's fragments and scale words overlap stage t's
-// 16 MFMAs.  Activation fragments are double-buffered (each is used by all of a stage's
-// MFMA rows); each weight fragment is read into its own registers right after its last
-// MFMA of the stage; with 32 fewer live VGPRs the block-scaled kernels no longer spill
-// (2 VGPRs still do in some per-tensor and bf16-activation instantiations).  Global data moves in pairs of stages through registers: one load
+// registers; the LDS reads of stage t+1's fragments overlap stage t's 16 MFMAs.
+// Activation fragments are double-buffered (each is used by all of a stage's MFMA rows);
+// each weight fragment is read into its own registers right after its last MFMA of the
+// stage; with 32 fewer live VGPRs the block-scaled kernels do not spill (2 VGPRs still
+// do in some per-tensor instantiations).  Each wave loads its own E8M0 scale words (16
+// bytes per operand and 128-wide K block) straight into registers two stages ahead.
+// Global data moves in pairs of stages through registers: one load
 // instruction brings whole 128-byte lines (both stages' halves of 8 rows).  An even
 // stage t writes the staged weight pair t+2, t+3 to LDS and loads the activation pair
 // t+4, t+5; the odd stage after it writes that pair and loads the next weight pair, so
@@ -63,12 +65,12 @@ typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
 constexpr int TILE = 256 * BK;  // bytes of one operand tile per stage (16 KB)
-constexpr int STILE = 1024;     // bytes of one operand's scale words per stage (256 rows)
-// One stage buffer: weight tile, activation tile, scales, and 64 bytes of padding.  LDS
-// banks repeat every 128 bytes; a staged store writes row r of buffers s and s + 1
-// from 8 neighbouring lanes (64 bytes each), which the padding puts in opposite halves
-// of the bank cycle (measured conflict-free; without it every store conflicts 2-way).
-constexpr int BUF = 2 * TILE + 2 * STILE + 64;
+// One stage buffer: weight tile, activation tile, room for the epilogue's 64-row output
+// slab, and 64 bytes of padding.  LDS banks repeat every 128 bytes; a staged store writes
+// row r of buffers s and s + 1 from 8 neighbouring lanes (64 bytes each), which the
+// padding puts in opposite halves of the bank cycle (measured conflict-free; without it
+// every store conflicts 2-way).
+constexpr int BUF = 2 * TILE + 2048 + 64;
 constexpr int EPI_ROW = 528;  // bytes of one staged 16-bit output row (512 + 16 pad, rows 16-byte aligned)
 static_assert(64 * EPI_ROW <= BUF, "an output slab must fit one stage buffer");
 
@@ -186,34 +188,6 @@ __device__ __forceinline__ void store_pair(const Loader& L, const v4u (&x)[8], u
     store_pair(L, x, tx, ty, std::make_integer_sequence<int, NP>{});
 }
 
-// Scale words of a pair of stages (one 128-wide K block): for a 256-row tile they are
-// two contiguous 512-byte chunks of the swizzled tensor (rows 128*rb .. +127), chunk
-// (rb * ncb + k0/128).  Wave w copies chunk rb = w & 1 of operand w >> 1 (0 = weight,
-// 1 = activation), 2 words per lane.  Inside a chunk row r's word sits at
-// (r % 32) * 16 + ((r % 128) / 32) * 4, so a lane's words for its four 32-row tiles are
-// one contiguous 16-byte LDS read.  Both stages of the pair get a copy.
-struct ScaleWords {
-    uint32_t s0, s1;
-};
-
-__device__ __forceinline__ void load_scales(ScaleWords& S, __amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a,
-                                            int rb0_b, int rb0_a, int ncb, int k0, int K, int wave, int lane) {
-    const int op = wave >> 1, rb = wave & 1;
-    const __amdgpu_buffer_rsrc_t rs = op ? rs_a : rs_b;
-    uint32_t chunk = static_cast<uint32_t>(((op ? rb0_a : rb0_b) + rb) * ncb + (k0 >> 7)) * 512u;
-    chunk = k0 < K ? chunk : 0x80000000u;  // stages past K: zero scale words
-    S.s0 = __builtin_amdgcn_raw_buffer_load_b32(rs, chunk + lane * 4, 0, 0);
-    S.s1 = __builtin_amdgcn_raw_buffer_load_b32(rs, chunk + 256 + lane * 4, 0, 0);
-}
-
-__device__ __forceinline__ void store_scales(const ScaleWords& S, uint8_t* sx, uint8_t* sy, int wave, int lane) {
-    const int off = (wave >> 1) * STILE + (wave & 1) * 512 + lane * 4;
-    *reinterpret_cast<uint32_t*>(sx + off) = S.s0;
-    *reinterpret_cast<uint32_t*>(sx + off + 256) = S.s1;
-    *reinterpret_cast<uint32_t*>(sy + off) = S.s0;
-    *reinterpret_cast<uint32_t*>(sy + off + 256) = S.s1;
-}
-
 // activation fragments of one stage (MFMA operand 1); the weight fragments (operand 0)
 // live in one v8i[NW] array
 struct Frags {
@@ -326,7 +300,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
 
     const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * p.K, min(TBN, p.N - n0), p.K, wave, lane, TBN / 4);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * p.K, min(BM, p.M - m0), p.K, wave, lane);
-    // scale words: waves 0, 1 move the weight's, waves 2, 3 the activation's
+    constexpr bool DS = !UNIT;  // block scales (per-tensor mode: E8M0 127 throughout)
     const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
@@ -343,53 +317,47 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         constexpr int B = decltype(b_c)::value & 3;
         return (B < 2 ? lds01 : lds23) + (B & 1) * BUF;
     };
-    // Register staging: a pair of stages of one operand (+ the pair's scale words with
-    // the weight) at a time.
+    // Register staging: a pair of stages of one operand at a time.
     v4u SB[8], SA[8];
-    ScaleWords SW;
-    auto load_b = [&](int s) {
-        load_pair<PB>(LB, SB, s * BK, p.K);
-        if constexpr (!UNIT) load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, s * BK, p.K, wave, lane);
+    auto load_b = [&](int s) { load_pair<PB>(LB, SB, s * BK, p.K); };
+    // Scale words: a lane's 4 words for its wave's 4 32-row tiles of an operand and one
+    // 128-wide K block (pair of stages) are 16 contiguous bytes of the swizzled tensor, at
+    // chunk ((row128 / 128) * ncb + pair) * 512 + r32 * 16 for the tiles' 128-row block
+    // row128.  Each wave loads its own into registers two stages ahead of use (staging them
+    // through LDS with the operands, shared by the workgroup, measured 1.3-1.8% slower on
+    // every shape, bit-identical).
+    const uint32_t dsb_off = static_cast<uint32_t>(((n0 >> 7) + (NW == 4 ? wn : 0)) * p.ncb * 512 + r32 * 16);
+    const uint32_t dsa_off = static_cast<uint32_t>(((m0 >> 7) + wm) * p.ncb * 512 + r32 * 16);
+    v4u DWB, DWA;  // words of the next pair not yet consumed
+    auto load_dscales = [&](int pair) {
+        const uint32_t po = pair < p.ncb ? static_cast<uint32_t>(pair * 512) : 0x80000000u;
+        DWB = __builtin_amdgcn_raw_buffer_load_b128(rssb, dsb_off + po, 0, 0);
+        DWA = __builtin_amdgcn_raw_buffer_load_b128(rssa, dsa_off + po, 0, 0);
     };
     auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
     const int hs = 8 * half;
-    // the weight scale chunk holding this wave's n rows, and its first 32-row tile there
-    const int sbc = NW == 4 ? wn : 0, sbt = NW == 4 ? 0 : 2 * wn;
-    auto read_scales = [&](auto b_c, uint32_t (&sb)[4], uint32_t (&sa)[4]) {
-        if constexpr (UNIT) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) sb[t] = sa[t] = 0x7f7f7f7fu;
-            return;
-        }
-        const uint8_t* st = buf(b_c) + 2 * TILE;
-        const v4u wb = *reinterpret_cast<const v4u*>(st + sbc * 512 + r32 * 16);
-        const v4u wa = *reinterpret_cast<const v4u*>(st + STILE + wm * 512 + r32 * 16);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sb[t] = (NW == 4 ? wb[t] : (sbt ? wb[2 + (t & 1)] : wb[t & 1])) >> hs;
-            sa[t] = wa[t] >> hs;
-        }
-    };
-
+    // the first of this wave's weight tiles in its 16-byte scale chunk (half tiles: 2 of 4)
+    const int sbt = NW == 4 ? 0 : 2 * wn;
     uint32_t scb[4], sca[4];
     Frags F0, F1;
     v8i FB[NW];
 
     // Stage t held in buffer B = t % 4 (compile-time): activation fragments F and the
     // weight fragments FB (stage t) are in registers; read stage t+1 into G and, each
-    // after its last MFMA here (slot 4i + 3), into FB[i].  A pair of stages (s, s+1), s even, moves in
-    // two halves: the activation pair is loaded at stage s-4 and written to LDS at
-    // s-3, the weight pair (with scales) loaded at s-3 and written at s-2.  Each write
-    // targets buffers whose previous stages were read before the current barrier.
+    // after its last MFMA here (slot 4i + 3), into FB[i].  A pair of stages (s, s+1), s
+    // even, moves in two halves: the activation pair is loaded at stage s-4 and written to
+    // LDS at s-3, the weight pair loaded at s-3 and written at s-2.  Each write targets
+    // buffers whose previous stages were read before the current barrier.  An odd stage
+    // shifts the next pair's scale words into place (slot SLOTS - 4) and loads the pair
+    // after it (slot SLOTS - 3).
     //
     // The stage is scheduled by hand in 16 slots, one MFMA each (sched_barrier keeps
-    // the order): the next stage's scale words first (their shifts 12 slots later, so
-    // no LDS latency is exposed), then its fragments in the order the next stage uses
-    // them, and in slots 0..7 one staged chunk written to LDS followed by the load that
-    // refills its registers, which therefore has a whole stage to arrive.  (Double-
+    // the order): the next stage's fragments in the order the next stage uses them, and
+    // in slots 0..7 one staged chunk written to LDS followed by the load that refills its
+    // registers, which therefore has a whole stage to arrive.  (Double-
     // buffering the weight fragments too gave the same times, bit-identical, but spilled
     // 2-3 VGPRs.)
     auto stage = [&](auto b_c, int t, Frags& F, Frags& G) {
@@ -404,17 +372,22 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         uint8_t* wx = EVEN ? buf(P2{}) : buf(P3{}) + TILE;
         uint8_t* wy = EVEN ? buf(P3{}) : buf(b_c) + TILE;
         const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, p.K) : pair_add(LB, (t + 3) * BK, p.K);
-        v4u wb, wa;
         uint32_t nb[4], na[4];
+        if constexpr (UNIT) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) nb[u] = na[u] = 0x7f7f7f7fu;
+        } else if constexpr (EVEN) {  // the next stage is in this stage's pair: same words
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                nb[u] = scb[u];
+                na[u] = sca[u];
+            }
+        }
         auto slot = [&](auto k_c) {
             constexpr int k = decltype(k_c)::value;
             constexpr int i = k / 4, j = k % 4;
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(FB[i], F.a[j], acc[i][j], 0, 0, OPSEL, scb[i],
                                                                         OPSEL, sca[j]);
-            if constexpr (k == 0 && !UNIT) {
-                wb = *reinterpret_cast<const v4u*>(nx + 2 * TILE + sbc * 512 + r32 * 16);
-                wa = *reinterpret_cast<const v4u*>(nx + 2 * TILE + STILE + wm * 512 + r32 * 16);
-            }
             if constexpr (k == 1) G.a[0] = read_frag(nx + TILE, faa);
             if constexpr (k >= 3 && k <= 5) G.a[k - 2] = read_frag(nx + TILE + (k - 2) * 32 * BK, faa);
             if constexpr (k % 4 == 3 && k / 4 < NW) FB[k / 4] = read_frag(nx + (k / 4) * 32 * BK, fab);
@@ -427,17 +400,15 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
                     if constexpr (k < PB) load_piece<k>(LB, SB, add);
                 }
             }
-            if constexpr (k == (SLOTS > 8 ? 8 : SLOTS - 1) && !UNIT) {
-                if constexpr (EVEN) store_scales(SW, buf(P2{}) + 2 * TILE, buf(P3{}) + 2 * TILE, wave, lane);
-                else load_scales(SW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, (t + 3) * BK, p.K, wave, lane);
-            }
-            if constexpr (k == SLOTS - 4) {
+            if constexpr (k == SLOTS - 4 && DS && !EVEN) {
+                // the next stage opens pair (t + 1) / 2: its words, then pair (t + 1) / 2 + 1's load
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    nb[u] = UNIT ? 0x7f7f7f7fu : (NW == 4 ? wb[u] : (sbt ? wb[2 + (u & 1)] : wb[u & 1])) >> hs;
-                    na[u] = UNIT ? 0x7f7f7f7fu : wa[u] >> hs;
+                    nb[u] = (NW == 4 ? DWB[u] : (sbt ? DWB[2 + (u & 1)] : DWB[u & 1])) >> hs;
+                    na[u] = DWA[u] >> hs;
                 }
             }
+            if constexpr (k == SLOTS - 3 && DS && !EVEN) load_dscales((t + 1) / 2 + 1);
             __builtin_amdgcn_sched_barrier(0);
         };
         for_each_index(slot, std::make_integer_sequence<int, SLOTS>{});
@@ -458,20 +429,28 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // write, so the prologue waits out one memory latency rather than two.
     {
         v4u XA[8], XB[8];
-        ScaleWords XW;
         load_a(0);
         load_pair<PB>(LB, XB, 0, p.K);
-        if constexpr (!UNIT) load_scales(XW, rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, 0, p.K, wave, lane);
+        if constexpr (DS) load_dscales(0);
         load_pair(LA, XA, 2 * BK, p.K);
         load_b(2);
         store_a(B0{}, B1{});
         store_pair<PB>(LB, XB, buf(B0{}), buf(B1{}));
-        if constexpr (!UNIT) store_scales(XW, buf(B0{}) + 2 * TILE, buf(B1{}) + 2 * TILE, wave, lane);
         store_pair(LA, XA, buf(B2{}) + TILE, buf(B3{}) + TILE);
     }
     stage_barrier<WAIT_LGKM0>();
     read_frags(F0, FB, lds01, fab, faa);
-    read_scales(B0{}, scb, sca);
+    if constexpr (DS) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            scb[u] = (NW == 4 ? DWB[u] : (sbt ? DWB[2 + (u & 1)] : DWB[u & 1])) >> hs;
+            sca[u] = DWA[u] >> hs;
+        }
+        load_dscales(1);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) scb[u] = sca[u] = 0x7f7f7f7fu;
+    }
 
     // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
     for (int t = 0; t < KT; t += 4) {
