@@ -204,7 +204,9 @@ int ckh_amax_scale(const void* x, int64_t numel, int in_code, float divisor, voi
  * (no hipMalloc, no torch allocator): for callers that cannot allocate, such as code
  * under hipGraph capture with no allocator of its own or serving loops that forbid
  * allocation.  Every input size fits (the grid never has more workgroups than the array
- * has words).  `stream` must belong to the current device.  All calls on one GPU share
+ * has words).  `stream` must belong to the current device.  The first call on a device
+ * resolves the array's address there (hipGetSymbolAddress) and must run outside stream
+ * capture; later calls may be captured into a hipGraph.  All calls on one GPU share
  * its array: calls that overlap on that GPU (other streams, other threads) race and must
  * be serialised by the caller.  No counterpart in the reference.
  */

@@ -3,11 +3,14 @@ checkpoint convention, made by the CPU oracle, with the oracle's expected output
 
     python tests/golden/make_checkpoints.py
 
-Keys follow the reference: per layer `<layer>.weight` (codes), `<layer>.weight_scale`
-(block scales, or the FP8 tensor scale), `<layer>.weight_scale_2` (NVFP4 tensor scale),
-`<layer>.input_scale` (NVFP4 static activation scale) and `<layer>.bias`, as
-samples/nvfp4_linear.py:39-61 loads them (its weight_scale is a flat uint8 tensor, which
-float8 checkpoints commonly use) and tensor/{fp8,mxfp8,nvfp4}.py serialise them.
+Keys, dtypes and shapes follow the reference layouts' state_dict_tensors
+(tensor/fp8.py:74-80, tensor/mxfp8.py:86-87, tensor/nvfp4.py:94-101): per layer
+`<layer>.weight` (codes: float8_e4m3fn [N, K], or uint8 [N, K/2] for NVFP4),
+`<layer>.weight_scale` (the FP8 tensor scale as a 0-dim fp32; the swizzled block scales as
+2-D float8_e8m0fnu / float8_e4m3fn), `<layer>.weight_scale_2` (the NVFP4 tensor scale, 0-dim
+fp32), plus `<layer>.input_scale` (NVFP4 static activation scale, fp32 [1], as
+samples/nvfp4_linear.py:93-99 writes it) and `<layer>.bias`; samples/nvfp4_linear.py:39-61
+loads them.
 
 Layers, each [N=128, K=256] from one bf16 weight `w_bf16`:
   fp8    TensorCoreFP8Layout, tensor scale amax/448
@@ -48,15 +51,13 @@ def make() -> dict[str, torch.Tensor]:
     qx = ref.quantize_per_tensor_fp8(x, sx.reshape(1))
     y = (ref.dequantize_per_tensor_fp8(qx, sx.reshape(1), torch.float32)
          @ ref.dequantize_per_tensor_fp8(qw, sw.reshape(1), torch.float32).T) + bias.float()
-    sd.update({"fp8.weight": qw.view(torch.uint8), "fp8.weight_scale": sw.reshape(1), "fp8.bias": bias,
-               "fp8.expected": y})
+    sd.update({"fp8.weight": qw, "fp8.weight_scale": sw.reshape(()), "fp8.bias": bias, "fp8.expected": y})
 
     # MXFP8 (tensor/mxfp8.py:86-87: "" and "_scale", E8M0 bytes swizzled)
     qw, bw = ref.quantize_mxfp8(w)
     qx, bx = ref.quantize_mxfp8(x)
     y = ref.scaled_mm_mxfp8_ref(qx, qw, bx, bw, out_dtype=torch.float32) + bias.float()
-    sd.update({"mxfp8.weight": qw.view(torch.uint8), "mxfp8.weight_scale": bw.view(torch.uint8),
-               "mxfp8.bias": bias, "mxfp8.expected": y})
+    sd.update({"mxfp8.weight": qw, "mxfp8.weight_scale": bw, "mxfp8.bias": bias, "mxfp8.expected": y})
 
     # NVFP4 (tensor/nvfp4.py:94-101; samples/nvfp4_linear.py:39-61)
     gw = ref.default_scale(w, 2688.0).reshape(1)
@@ -67,9 +68,9 @@ def make() -> dict[str, torch.Tensor]:
     g_in = (gx * 1.25).reshape(1)  # a calibrated static input scale, not the dynamic one
     qs, bs = ref.quantize_nvfp4(x, g_in)
     y_static = ref.scaled_mm_nvfp4_ref(qs, qw, g_in, gw, bs, bw, out_dtype=torch.float32) + bias.float()
-    sd.update({"nvfp4.weight": qw, "nvfp4.weight_scale": bw.view(torch.uint8).reshape(-1),
-               "nvfp4.weight_scale_2": gw, "nvfp4.input_scale": g_in, "nvfp4.bias": bias,
-               "nvfp4.expected": y, "nvfp4.expected_static": y_static})
+    sd.update({"nvfp4.weight": qw, "nvfp4.weight_scale": bw, "nvfp4.weight_scale_2": gw.reshape(()),
+               "nvfp4.input_scale": g_in, "nvfp4.bias": bias, "nvfp4.expected": y,
+               "nvfp4.expected_static": y_static})
     return {k: v.contiguous().clone() for k, v in sd.items()}
 
 

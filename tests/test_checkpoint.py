@@ -144,9 +144,9 @@ def test_golden_checkpoint_is_what_the_oracle_writes():
 
 def _load_layer(st, name, device):
     """Rebuild a layer's weight the way the reference's loaders do: codes from `weight`, the
-    NVFP4 block scales from the flat uint8 `weight_scale` viewed as e4m3 with `weight_scale_2`
-    as the tensor scale (samples/nvfp4_linear.py:39-61); FP8 / MXFP8 scales from
-    `weight_scale` (tensor/fp8.py:74-80, tensor/mxfp8.py:86-87)."""
+    NVFP4 block scales from `weight_scale` viewed as e4m3 with `weight_scale_2` as the tensor
+    scale (samples/nvfp4_linear.py:39-61); FP8 / MXFP8 scales from `weight_scale`
+    (tensor/fp8.py:74-80, tensor/mxfp8.py:86-87)."""
     w = st["w_bf16"]
     shape = tuple(w.shape)
     codes = st[f"{name}.weight"].to(device)
@@ -191,15 +191,12 @@ def test_golden_checkpoint_linear_matches_the_oracle(name, static, hip):
 @pytest.mark.parametrize("name", ["fp8", "mxfp8", "nvfp4"])
 def test_golden_checkpoint_bytes_from_the_gpu_quantizers(name, hip):
     """Quantizing the checkpoint's source weight on the GPU through the layout reproduces the
-    committed codes and scales bit for bit."""
+    committed state-dict tensors: the same keys, dtypes, shapes and bytes."""
     st = _golden()
     qt = QuantizedTensor.from_float(st["w_bf16"].cuda(), LAYOUTS[name])
     sd = {k: v.cpu() for k, v in qt.state_dict("weight").items()}
-    assert torch.equal(_bits(sd["weight"]), st[f"{name}.weight"])
-    if name == "nvfp4":
-        assert torch.equal(_bits(sd["weight_scale"]).reshape(-1), st["nvfp4.weight_scale"])
-        assert torch.equal(sd["weight_scale_2"].reshape(1), st["nvfp4.weight_scale_2"])
-    elif name == "mxfp8":
-        assert torch.equal(_bits(sd["weight_scale"]), st["mxfp8.weight_scale"])
-    else:
-        assert torch.equal(sd["weight_scale"].reshape(1), st["fp8.weight_scale"])
+    keys = {"weight", "weight_scale", "weight_scale_2"} if name == "nvfp4" else {"weight", "weight_scale"}
+    assert set(sd) == keys
+    for k in keys:
+        assert _same(sd[k], st[f"{name}.{k}"]), (k, sd[k].dtype, tuple(sd[k].shape), st[f"{name}.{k}"].dtype,
+                                                 tuple(st[f"{name}.{k}"].shape))

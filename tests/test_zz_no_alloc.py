@@ -47,3 +47,38 @@ def test_no_alloc_matches_workspace_entry_point(dtype, divisor, hip):
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int32), want.view(torch.int32)), (float(got), float(want))
     assert float(got) == float((torch.amax(small[1:].abs().cuda()) / divisor).float())
+
+
+def test_no_alloc_under_graph_capture(hip):
+    """The callers it is for: captured in a HIP graph (after one eager call on the device,
+    which resolves the array's address), two calls of different sizes, the graph replayed
+    several times with eager work that changes the inputs between replays; every replay's
+    scales equal the workspace entry point's on the same inputs."""
+    lib = hb.load_library()
+    g = torch.Generator().manual_seed(11)
+    big = torch.randn(4096 * 3072, generator=g).bfloat16().cuda()
+    small = (torch.randn(70_001, generator=g) * 3).bfloat16().cuda()
+    _no_alloc(lib, small, 448.0)  # the first call on this device: outside capture
+    torch.cuda.synchronize()
+    outs = [torch.zeros((), dtype=torch.float32, device="cuda") for _ in range(2)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for x, o in zip((big, small), outs):
+                rc = lib.ckh_amax_scale_noalloc(x.data_ptr(), x.numel(), DTYPE_TO_CODE[x.dtype], 448.0, o.data_ptr(),
+                                                stream.cuda_stream)
+                assert rc == 0, lib.ckh_last_error()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        big.mul_(1.5 if rep % 2 else 0.75)
+        small[rep * 1000] = 50.0 * (rep + 1)  # the small input's amax changes every replay
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for x, o in zip((big, small), outs):
+            want = _with_workspace(lib, x, 448.0)
+            torch.cuda.synchronize()
+            assert torch.equal(o.view(torch.int32), want.view(torch.int32)), (rep, float(o), float(want))
+    assert float(outs[1]) == float((torch.amax(small.abs()) / 448.0).float())
