@@ -54,15 +54,32 @@ def hipcc() -> str:
     return cand
 
 
+# Most per-lane scratch (private memory) bytes a kernel may use.  A private array the
+# compiler fails to keep in registers (e.g. behind a call it did not inline) lands in scratch
+# memory and can make a kernel ten times slower without changing its results; the build
+# fails instead.  The MXFP8 tile kernel spills 2-3 registers in some instantiations (12 bytes).
+SCRATCH_LIMIT = 16
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    lines = [l for l in res.stderr.splitlines() if noise not in l]
+    err = "\n".join(l for l in lines if "kernel-resource-usage" not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
+    kernel = "?"
+    for l in lines:
+        if "Function Name:" in l:
+            kernel = l.split("Function Name:")[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in l:
+            n = int(l.split("ScratchSize [bytes/lane]:")[1].split()[0])
+            if n > SCRATCH_LIMIT:
+                raise RuntimeError(f"{src.name}: kernel {kernel} uses {n} bytes/lane of scratch "
+                                   f"(limit {SCRATCH_LIMIT}): a private array left memory-resident")
 
 
 def _link(sources: list[Path], out: Path, objdir: Path, verbose: bool) -> Path:

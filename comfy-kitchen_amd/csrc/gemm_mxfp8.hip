@@ -52,6 +52,7 @@
 #include <utility>
 
 #include "ckh_common.h"
+#include "skinny.h"
 
 namespace ckh {
 namespace mx {
@@ -585,14 +586,8 @@ namespace sk {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kSkChunk = 4;              // K steps (64 bytes) per wave per chunk: two scale words
-constexpr int kSkRow = 64 * kSkChunk;    // staged bytes per row and chunk (256)
-constexpr int kSkCpr = kSkRow / 16;      // 16-byte chunks per staged row
-constexpr int kSkRpl = 1024 / kSkRow;    // staged rows per direct-to-LDS load (1 KB)
-constexpr int kAuxNontemporal = 2;       // buffer-load cache policy bit: the weight is read once
+constexpr int kSkChunk = kSkRow / 64;    // K steps (64 bytes) per wave per chunk: two scale words
 
 struct Args {
     const uint8_t* a;
@@ -608,33 +603,11 @@ struct Args {
     const float* tsb;
 };
 
-// Staging layout: row r of a chunk is 256 bytes; logical 16-byte chunk c sits at physical
-// chunk c ^ (r % 16).  LDS banks repeat every 256 bytes, so a fragment read (16 lanes = 16
-// consecutive rows, one logical chunk) hits 16 distinct 16-byte bank groups.
-__device__ __forceinline__ uint32_t sk_swz(int r) { return static_cast<uint32_t>(r & (kSkCpr - 1)); }
-
-// Direct-to-LDS whole-line loads of rows [0, NQ * kSkRpl) of a chunk: load q writes 1 KB,
-// rows kSkRpl q .. , lane i to row kSkRpl q + i / kSkCpr, physical chunk i % kSkCpr, so each
-// load reads 8 whole 128-byte lines.  Bytes past K, and rows outside the descriptor, arrive
-// as zeros.
-template <int NQ, int AUX>
-__device__ __forceinline__ void stage_rows(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int K, int kbase, int lane) {
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-        const int row = kSkRpl * q + lane / kSkCpr;
-        const int k = kbase + static_cast<int>(((lane % kSkCpr) ^ sk_swz(row)) << 4);
-        const uint32_t off = k < K ? static_cast<uint32_t>(row * K + k) : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + q * 1024), 16, off, 0, 0, AUX);
-    }
-}
-
 // This lane's MFMA operand for step j of the staged chunk: row r, logical chunks 4 j + h and
 // 4 j + 2 + h (bytes k0 + 16 h and k0 + 32 + 16 h of the step).
 __device__ __forceinline__ v8i staged_frag(const uint8_t* st, int r, int h, int j) {
-    const uint8_t* row = st + r * kSkRow;
-    const uint32_t s = sk_swz(r);
-    const v4u x = *reinterpret_cast<const v4u*>(row + (((4 * j + h) ^ s) << 4));
-    const v4u y = *reinterpret_cast<const v4u*>(row + (((4 * j + 2 + h) ^ s) << 4));
+    const v4u x = staged_chunk(st, r, 4 * j + h);
+    const v4u y = staged_chunk(st, r, 4 * j + 2 + h);
     return v8i{(int)x[0], (int)x[1], (int)x[2], (int)x[3], (int)y[0], (int)y[1], (int)y[2], (int)y[3]};
 }
 
@@ -669,12 +642,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
-    // row group of this workgroup: the groups are dealt so that each XCD (blockIdx % 8) runs a
-    // contiguous range of them, so the 32-row groups that share a 128-row block of swizzled
-    // scale lines run on one XCD (its L2 fetches those lines once)
-    int grp = blockIdx.x;
-    if ((gridDim.x & 7) == 0) grp = (grp & 7) * (gridDim.x >> 3) + (grp >> 3);
-    const int n0 = grp * WR;
+    const int n0 = xcd_group(blockIdx.x, gridDim.x) * WR;
 
     const __amdgpu_buffer_rsrc_t rb =
         buffer_rsrc(p.b + static_cast<int64_t>(n0) * p.K, static_cast<uint32_t>(min(WR, p.N - n0)) * p.K);

@@ -44,6 +44,7 @@
 
 #include "ckh_common.h"
 #include "quant_math.h"
+#include "skinny.h"
 
 namespace ckh {
 namespace nv {
@@ -421,9 +422,410 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
 }
 
 }  // namespace nv
+
+// ------------------------------------------------------------ skinny activations
+// GEMMs with few activation rows (M <= 64) stream the weight once and are bound by HBM
+// bandwidth on it; the 256 x 256 tiles above would give them only N / 256 workgroups.  A
+// workgroup owns 32 or 64 weight rows and all of K; its waves split K in chunks of 128 code
+// bytes per row (256 elements: 4 stages of 64, 4 scale words per row), chunk c to wave
+// c % WV, and each wave keeps two chunks in flight: its weight rows go to one of two LDS
+// buffers by whole-line direct-to-LDS loads, scale words and activation codes to registers,
+// and the loads of chunk i + 2 are issued as soon as chunk i's LDS reads are done.
+//
+// Operands are decoded to fp16 as in the tile kernel (lane l = 32 h + r: row r, code bytes
+// 16 h .. 16 h + 15 of each 32-byte stage, dword kk for MFMA substep kk, whose block scale is
+// byte 2 h + kk / 2 of the row's scale word) and multiplied with v_mfma_f32_32x32x16_f16.
+// With M <= 16 most of a 32-row MFMA operand is padding, so the activation (AR = 8 or 16
+// rows) is decoded once per chunk by the whole wave, 32 elements a lane, into an fp16 area
+// of LDS, and its fragments are read from there; lanes of rows past AR read a zero row.
+// Larger M decode their activation fragments in registers, each feeding NT MFMAs.  At the
+// end the K partials meet in LDS and each wave adds and stores its share of the tile, times
+// alpha, plus bias.  Rows past M or N, bytes past K and scale columns past the last read as
+// zeros.
+namespace nvsk {
+
+using ckh::v8h;
+using ckh::v2h;
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kCb = 128;             // code bytes per row and chunk
+constexpr int kStages = kCb / 32;    // 64-element stages (and scale words of a row) per chunk: 4
+constexpr int kApitch = 2 * 2 * kCb + 16;  // bytes of one decoded fp16 activation row (+16 pad)
+constexpr int kAuxNontemporal = 2;   // buffer-load cache policy bit: the weight is read once
+
+struct Args {
+    const uint8_t* a;
+    const uint8_t* b;
+    const uint8_t* sa;
+    const uint8_t* sb;
+    const float* alpha;
+    const void* bias;
+    void* out;
+    int M, N, K;           // K in elements
+    int ncb;               // scale word columns: ceil(K/16/4)
+    int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
+};
+
+// Staged weight rows are 128 bytes; logical 16-byte chunk c of row r sits at physical chunk
+// c ^ (r % 8) ^ ((r / 8) % 2), so the 16 rows of a fragment read (one logical chunk each)
+// hit 16 distinct 16-byte groups of the 256-byte bank cycle.
+__device__ __forceinline__ uint32_t swz8(int r) { return static_cast<uint32_t>((r & 7) ^ ((r >> 3) & 1)); }
+
+// Direct-to-LDS loads of a chunk of 32 NT weight rows: load q writes 1 KB (rows 8 q .. 8 q + 7),
+// lane i to row 8 q + i / 8, physical chunk i % 8, i.e. 8 whole 128-byte lines per load.
+template <int NQ>
+__device__ __forceinline__ void stage_weight(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int Kb, int b0, int lane) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int row = 8 * q + (lane >> 3);
+        const int k = b0 + static_cast<int>(((lane & 7) ^ swz8(row)) << 4);
+        const uint32_t off = k < Kb ? static_cast<uint32_t>(row * Kb + k) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + q * 1024), 16, off, 0, 0, kAuxNontemporal);
+    }
+}
+
+// One chunk's register-held operands.
+template <int NT, int MT, int AR>
+struct Regs {
+    uint32_t swb[kStages][NT];  // weight scale words, one per stage
+    // AR > 0: the lane's 32 activation elements (row 8 s + lane / 8, 16-byte chunk lane % 8)
+    // of each group s of 8 rows, and their scale words
+    v4u ac[AR > 0 ? AR / 8 : 1];
+    uint32_t aw[AR > 0 ? AR / 8 : 1];
+    // AR == 0: 16 activation code bytes per stage and tile, and the tiles' scale words
+    v4u al[AR > 0 ? 1 : MT][kStages];
+    uint32_t swa[kStages][AR > 0 ? 1 : MT];
+};
+
+// Pin a chunk's registers at this point: the empty asm "modifies" them, so nothing computed
+// from them (e.g. a scale pair) can be hoisted into an earlier step, where it would make the
+// compiler wait for that chunk's loads.
+template <int NT, int MT, int AR>
+__device__ __forceinline__ void pin(Regs<NT, MT, AR>& R) {
+#pragma unroll
+    for (int j = 0; j < kStages; ++j) {
+#pragma unroll
+        for (int u = 0; u < NT; ++u) __asm__ volatile("" : "+v"(R.swb[j][u]));
+    }
+    if constexpr (AR > 0) {
+#pragma unroll
+        for (int s = 0; s < AR / 8; ++s) __asm__ volatile("" : "+v"(R.ac[s]), "+v"(R.aw[s]));
+    } else {
+#pragma unroll
+        for (int j = 0; j < kStages; ++j) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t) __asm__ volatile("" : "+v"(R.al[t][j]), "+v"(R.swa[j][t]));
+        }
+    }
+}
+
+// vector-memory instructions issue() makes per chunk (for the vmcnt waits)
+template <int NT, int MT, int AR>
+constexpr int loads_per_chunk() {
+    return 4 * NT + kStages + (AR > 0 ? 2 * (AR / 8) : MT * kStages + kStages);
+}
+
+// n consecutive scale words (n = 1 or 2) from offset off of a swizzled scale tensor
+template <int N>
+__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[N]) {
+    if constexpr (N == 2) {
+        const v2u x = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+        w[0] = x[0];
+        w[1] = x[1];
+    } else {
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    }
+}
+
+__device__ __forceinline__ v2h bcast(_Float16 x) { return v2h{x, x}; }
+
+template <int WAITCNT>
+__device__ __forceinline__ void wait() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(WAITCNT);
+    __asm__ volatile("" ::: "memory");
+}
+
+// WV: waves per workgroup, each taking every WV-th K chunk.
+// NT: 32-row weight tiles per workgroup (1 or 2).
+// MT: 32-row activation tiles (M <= 32 MT).
+// AR: activation rows decoded once per chunk into LDS (8 or 16, >= M, MT = 1), or 0: the
+// activation fragments are decoded in registers.
+// D: chunks in flight per wave (LDS weight buffers).
+template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D>
+__global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
+    static_assert(AR == 0 || (MT == 1 && AR % 8 == 0 && AR <= 16), "decoded activation: 8 or 16 rows");
+    static_assert(16 % WV == 0, "each wave stores 16 / WV accumulator registers");
+    static_assert(NT <= 2 && MT <= 2, "scale words of at most two tiles per load");
+    constexpr int WR = 32 * NT;                                   // weight rows of the workgroup
+    constexpr int WB = WR * kCb;                                  // one staged weight chunk
+    constexpr int WST = D * WB + (AR > 0 ? AR * kApitch : 0);     // LDS per wave
+    constexpr int ZERO = AR > 0 ? kApitch : 0;                    // the zero activation row
+    constexpr int RED = WV * NT * MT * 16 * 64 * 4;
+    constexpr int LDS = WV * WST + ZERO > RED ? WV * WST + ZERO : RED;
+    constexpr int LPC = loads_per_chunk<NT, MT, AR>();
+    static_assert((D - 1) * LPC < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5, r = lane & 31;
+    const int n0 = sk::xcd_group(blockIdx.x, gridDim.x) * WR;
+    const int Kb = p.K / 2;  // code bytes per row
+
+    const __amdgpu_buffer_rsrc_t rb =
+        buffer_rsrc(p.b + static_cast<int64_t>(n0) * Kb, static_cast<uint32_t>(min(WR, p.N - n0)) * Kb);
+    __amdgpu_buffer_rsrc_t ra[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        ra[t] = buffer_rsrc(p.a + static_cast<int64_t>(32 * t) * Kb,
+                            static_cast<uint32_t>(max(0, min(32, p.M - 32 * t))) * Kb);
+    const __amdgpu_buffer_rsrc_t rsb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
+    const __amdgpu_buffer_rsrc_t rsa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
+    // Scale word of row r of the workgroup's first weight tile in word column c: swizzled
+    // offset ((row/128 * ncb + c) * 32 + row%32) * 16 + ((row%128)/32) * 4; the second tile's
+    // word follows it (n0 is a multiple of 64 when NT = 2).  Activation row i (< 128):
+    // (i%32) * 16 + (i/32) * 4.
+    const uint32_t sb_row = static_cast<uint32_t>((n0 >> 7) * p.ncb * 512 + r * 16 + ((n0 & 127) >> 5) * 4);
+    const int NC = (Kb + kCb - 1) / kCb;
+
+    uint8_t* wbuf = lds + wave * WST;           // this wave's D weight buffers
+    uint8_t* actf = wbuf + D * WB;              // its decoded activation rows (AR > 0)
+    uint8_t* zrow = lds + WV * WST;             // zero row shared by the workgroup (AR > 0)
+    if constexpr (AR > 0) {
+        for (int i = threadIdx.x; i < kApitch / 4; i += 64 * WV) reinterpret_cast<uint32_t*>(zrow)[i] = 0u;
+        __syncthreads();
+    }
+
+    // (the lambdas are forced inline: an outlined step would keep R in scratch memory)
+    auto issue = [&](int c, uint8_t* buf, Regs<NT, MT, AR>& R) __attribute__((always_inline)) {
+        const int b0 = c * kCb;  // first code byte of the chunk
+        stage_weight<4 * NT>(rb, buf, Kb, b0, lane);
+#pragma unroll
+        for (int j = 0; j < kStages; ++j) {
+            const int col = c * kStages + j;
+            const uint32_t co = col < p.ncb ? static_cast<uint32_t>(col * 512) : 0x80000000u;
+            load_words<NT>(rsb, sb_row + co, R.swb[j]);
+        }
+        if constexpr (AR > 0) {
+            const int q = lane & 7;
+#pragma unroll
+            for (int s = 0; s < AR / 8; ++s) {
+                const int row = 8 * s + (lane >> 3);
+                const int k = b0 + 16 * q;
+                R.ac[s] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      ra[0], k < Kb ? static_cast<uint32_t>(row * Kb + k) : 0x80000000u,
+                                                      0, 0));
+                const int col = c * kStages + (q >> 1);
+                R.aw[s] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rsa, col < p.ncb ? static_cast<uint32_t>(col * 512 + row * 16) : 0x80000000u, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kStages; ++j) {
+                const int col = c * kStages + j;
+                const uint32_t co = col < p.ncb ? static_cast<uint32_t>(col * 512) : 0x80000000u;
+                load_words<MT>(rsa, r * 16 + co, R.swa[j]);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int j = 0; j < kStages; ++j) {
+                    const int k = b0 + 32 * j + 16 * h;
+                    R.al[t][j] = __builtin_bit_cast(
+                        v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                 ra[t], k < Kb ? static_cast<uint32_t>(r * Kb + k) : 0x80000000u, 0, 0));
+                }
+        }
+    };
+
+    v16f acc[NT][MT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[u][t] = v16f{};
+
+    // lane's fragment addresses: weight row r of tile u, logical chunk 2 j + h; decoded
+    // activation row r (or the zero row), bytes 128 j + 64 h + 16 kk
+    const uint32_t wrow = static_cast<uint32_t>(r * kCb);
+    const uint32_t wsw = swz8(r);
+    const uint8_t* abase = (AR > 0 && r < AR ? actf + r * kApitch : zrow) + 64 * h;
+
+    auto compute = [&](const uint8_t* buf, const Regs<NT, MT, AR>& R) __attribute__((always_inline)) {
+        if constexpr (AR > 0) {
+            // decode the chunk's activation rows: lane's 32 elements are blocks 2 q, 2 q + 1 of
+            // the chunk (bytes 2 (q % 2), +1 of word q / 2)
+            const int q = lane & 7;
+#pragma unroll
+            for (int s = 0; s < AR / 8; ++s) {
+                const v2h sp = scale_pair(R.aw[s], 16 * (q & 1));
+                uint8_t* dst = actf + (8 * s + (lane >> 3)) * kApitch + q * 64;
+                *reinterpret_cast<v8h*>(dst) = decode8(R.ac[s][0], bcast(sp[0]));
+                *reinterpret_cast<v8h*>(dst + 16) = decode8(R.ac[s][1], bcast(sp[0]));
+                *reinterpret_cast<v8h*>(dst + 32) = decode8(R.ac[s][2], bcast(sp[1]));
+                *reinterpret_cast<v8h*>(dst + 48) = decode8(R.ac[s][3], bcast(sp[1]));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kStages; ++j) {
+            v4u cb[NT];
+            v2h pb[NT];
+#pragma unroll
+            for (int u = 0; u < NT; ++u) {
+                cb[u] = *reinterpret_cast<const v4u*>(buf + u * 32 * kCb + wrow + (((2 * j + h) ^ wsw) << 4));
+                pb[u] = scale_pair(R.swb[j][u], 16 * h);
+            }
+            v2h pa[MT];
+            if constexpr (AR == 0) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t) pa[t] = scale_pair(R.swa[j][t], 16 * h);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                v8h da[MT];
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    if constexpr (AR > 0) da[t] = *reinterpret_cast<const v8h*>(abase + 128 * j + 16 * kk);
+                    else da[t] = decode8(R.al[t][j][kk], bcast(pa[t][kk >> 1]));
+                }
+#pragma unroll
+                for (int u = 0; u < NT; ++u) {
+                    const v8h db = decode8(cb[u][kk], bcast(pb[u][kk >> 1]));
+#pragma unroll
+                    for (int t = 0; t < MT; ++t)
+                        acc[u][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(db, da[t], acc[u][t], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // This wave's chunks c_i = wave + i WV, i < n.  Chunks i .. i + D - 1 are in flight while
+    // chunk i is computed (buffer i % D, registers R[i % D]).  Every step issues the loads
+    // of chunk i + D, past the end too (they read nothing and write zeros to its own
+    // buffer), so that when a step starts exactly D - 1 chunks' loads follow its own and the
+    // wait count is the same on every path, including the compiler's own counting for the
+    // registers of each R[d].
+    const int n = wave < NC ? (NC - wave + WV - 1) / WV : 0;
+    Regs<NT, MT, AR> R[D];
+    nv::for_each_index([&](auto d_c) {
+        constexpr int d = decltype(d_c)::value;
+        issue(wave + d * WV, wbuf + d * WB, R[d]);
+    }, std::make_integer_sequence<int, D>{});
+    auto step = [&](int i, auto d_c) __attribute__((always_inline)) {
+        constexpr int d = decltype(d_c)::value;
+        wait<nv::waitcnt_vm_lgkm0((D - 1) * LPC)>();  // chunk i's loads are done
+        pin(R[d]);
+        compute(wbuf + d * WB, R[d]);
+        // the loads of chunk i + D overwrite this buffer: every read of it is done
+        wait<nv::waitcnt_vm_lgkm0(63)>();
+        issue(wave + (i + D) * WV, wbuf + d * WB, R[d]);
+    };
+    int i = 0;
+    for (; i + D - 1 < n; i += D)
+        nv::for_each_index([&](auto d_c) { step(i + decltype(d_c)::value, d_c); }, std::make_integer_sequence<int, D>{});
+    // the last n % D chunks
+    nv::for_each_index([&](auto d_c) {
+        if (i + decltype(d_c)::value < n) step(i + decltype(d_c)::value, d_c);
+    }, std::make_integer_sequence<int, D - 1>{});
+    wait<nv::waitcnt_vm_lgkm0(0)>();  // the trailing loads write LDS, which is reused below
+
+    // the K partials of each 32 x 32 tile meet in LDS (reusing the staging area); wave w adds
+    // and stores registers RPW w .. RPW w + RPW - 1 (columns n0 + 32 u + 8 (v / 4) + 4 h + v % 4
+    // of row m = 32 t + r)
+    constexpr int RPW = 16 / WV;
+    __syncthreads();
+    float (*red)[NT][MT][16][64] = reinterpret_cast<float (*)[NT][MT][16][64]>(lds);
+#pragma unroll
+    for (int u = 0; u < NT; ++u)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[wave][u][t][v][lane] = acc[u][t][v];
+    __syncthreads();
+    const float alpha = p.alpha[0];
+    const int v0 = RPW * wave;
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int n = n0 + 32 * u + 8 * (v0 >> 2) + 4 * h + (v0 & 3);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int m = 32 * t + r;
+            float v[RPW];
+#pragma unroll
+            for (int e = 0; e < RPW; ++e) {
+                float s = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WV; ++w) s += red[w][u][t][v0 + e][lane];
+                v[e] = s * alpha + (n + e < p.N ? nv::bias_at<BIAS>(p.bias, n + e) : 0.0f);
+            }
+            if (m >= p.M) continue;
+            const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+            if constexpr (RPW == 4) {
+                if (n + 3 < p.N && (p.N & 3) == 0) {
+                    nv::store4<OUT>(p.out, idx, v);
+                    continue;
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < RPW; ++e)
+                if (n + e < p.N) nv::store1<OUT>(p.out, idx + e, v[e]);
+        }
+    }
+}
+
+}  // namespace nvsk
 }  // namespace ckh
 
 using namespace ckh;
+
+namespace {
+
+// Activations of at most kNvSkinnyMaxM rows take the skinny kernel (nvsk::gemm_skinny_kernel).
+constexpr int kNvSkinnyMaxM = 64;
+
+int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    nvsk::Args p{};
+    p.a = q.a; p.b = q.b; p.sa = q.sa; p.sb = q.sb; p.alpha = q.alpha; p.bias = q.bias; p.out = q.out;
+    p.M = q.M; p.N = q.N; p.K = q.K; p.ncb = q.ncb; p.sa_rows = q.sa_rows; p.sb_rows = q.sb_rows;
+    // Per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
+    // activation rows decoded to LDS, chunks in flight per wave.  Measured (graph-timed, K = 5120,
+    // N = 13824): M = 1 12.5 us, M = 8 13.0 us, M = 16 16.0 us; 8 waves, 3 chunks in flight, or
+    // activation fragments decoded in registers were 10-20% slower at M <= 8.  For M > 16 two
+    // weight tiles per workgroup halve the activation decoding per weight byte, which pays
+    // while N gives enough workgroups (M = 64: N = 13824 19.4 against 24.8 us with one tile;
+    // N = 5120, K = 13824 27.5 against 32.4 us with two).
+    const bool two = q.N >= 8192;
+#define LAUNCH(O, B, WV, NT, MT, AR, D)                                                           \
+    hipLaunchKernelGGL((nvsk::gemm_skinny_kernel<O, B, WV, NT, MT, AR, D>),                       \
+                       dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
+#define BY_MT(O, B)                                            \
+    do {                                                       \
+        if (p.M <= 8) LAUNCH(O, B, 4, 1, 1, 8, 2);             \
+        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16, 2);      \
+        else if (p.M <= 32 && two) LAUNCH(O, B, 4, 2, 1, 0, 2); \
+        else if (p.M <= 32) LAUNCH(O, B, 4, 1, 1, 0, 2);       \
+        else if (two) LAUNCH(O, B, 4, 2, 2, 0, 2);             \
+        else LAUNCH(O, B, 4, 1, 2, 0, 2);                      \
+    } while (0)
+#define BY_BIAS(O)                                          \
+    do {                                                    \
+        if (!has_bias) BY_MT(O, -1);                        \
+        else if (bias_code == CKH_F32) BY_MT(O, CKH_F32);   \
+        else if (bias_code == CKH_F16) BY_MT(O, CKH_F16);   \
+        else BY_MT(O, CKH_BF16);                            \
+    } while (0)
+    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+    else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef BY_MT
+#undef LAUNCH
+    return check_launch("scaled_mm_nvfp4");
+}
+
+}  // namespace
 
 extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void* sb, const void* alpha,
                                    const void* bias, void* out, int64_t M, int64_t N, int64_t K, int out_code,
@@ -457,8 +859,9 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
     p.sb_rows = static_cast<int>(rup(N, 128));
     p.tiles_m = static_cast<int>(cdiv(M, nv::BM));
     p.tiles_n = static_cast<int>(cdiv(N, nv::BN));
-    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (p.M <= kNvSkinnyMaxM) return launch_nv_skinny(p, out_code, bias_code, bias != nullptr, st);
+    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
 #define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_kernel<O, B>), grid, dim3(nv::NT), 0, st, p)
 #define BY_BIAS(O)                                         \
     do {                                                   \

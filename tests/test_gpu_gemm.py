@@ -189,13 +189,58 @@ def test_scaled_mm_nvfp4_bias_and_alpha(bias_dtype, hip):
     assert rel_l2(got2, want2) <= REL_L2[torch.float32]
 
 
-def test_scaled_mm_nvfp4_hi_first_invariance(hip):
-    """Packing order does not change the product when both operands share it."""
-    qx, sx, gx, qw, sw, gw = nv_operands(128, 256, 512, seed=2)
+@pytest.mark.parametrize("m", [128, 5])
+def test_scaled_mm_nvfp4_hi_first_invariance(m, hip):
+    """Packing order does not change the product when both operands share it (tile and
+    skinny kernels)."""
+    qx, sx, gx, qw, sw, gw = nv_operands(m, 256, 512, seed=2)
     a = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.float32)
     b = ck.scaled_mm_nvfp4(ck.swap_nibbles(qx).cuda(), ck.swap_nibbles(qw).cuda(), gx.cuda(), gw.cuda(), sx.cuda(),
                            sw.cuda(), out_dtype=torch.float32)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 3072), (8, 200, 288), (9, 64, 1024), (16, 1000, 3072), (17, 1000, 3072),
+                                   (31, 96, 224), (32, 4096, 64), (33, 130, 5120), (40, 33, 96), (64, 512, 1056),
+                                   (2, 33, 32), (48, 13824, 128), (3, 160, 1536), (20, 8200, 256), (40, 8192, 96),
+                                   (12, 40, 4096)])
+def test_scaled_mm_nvfp4_skinny(m, n, k, out_dtype, hip):
+    """At most 64 activation rows take the skinny NVFP4 kernel (a workgroup per 32 or 64
+    weight rows, K split over its waves in chunks of 256 elements, two chunks in flight per
+    wave; configurations by M (boundaries 8 / 16 / 32 / 64) and, past 16 rows, by N (two weight
+    tiles from N = 8192)): rows past M, columns past N, K % 64 == 32 (a half-used scale word),
+    fewer chunks than waves, K past one chunk round and long K."""
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=m * 13 + n + k)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("m", [1, 12, 20, 40])
+def test_scaled_mm_nvfp4_skinny_bias_and_alpha(bias_dtype, m, hip):
+    """The skinny NVFP4 epilogue: alpha times the sum, plus bias of each dtype."""
+    n, k = 300, 640
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=m + 91)
+    bias = (torch.randn(n) * 0.1).to(bias_dtype)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), bias=bias.cuda(),
+                             out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+
+
+def test_scaled_mm_nvfp4_skinny_matches_tile_rows(hip):
+    """Rows of a 65-row product (tile kernel) against the same rows computed alone (skinny
+    kernel): both sum exact fp16 products in fp32 MFMAs, so they agree to fp32 rounding."""
+    qx, sx, gx, qw, sw, gw = nv_operands(65, 512, 2048, seed=44)
+    full = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.float32)
+    part_s = ref.to_blocked(ref.from_blocked(sx.view(torch.uint8), 65, 2048 // 16)[:7].contiguous()).view(
+        torch.float8_e4m3fn)
+    part = ck.scaled_mm_nvfp4(qx[:7].cuda(), qw.cuda(), gx.cuda(), gw.cuda(), part_s.cuda(), sw.cuda(),
+                              out_dtype=torch.float32)
+    assert rel_l2(part, full[:7]) <= 1e-5
 
 
 def test_scaled_mm_nvfp4_config5_full(hip):
@@ -213,3 +258,13 @@ def test_scaled_mm_nvfp4_config5_full(hip):
     r = ((got.float() - want).norm() / want.norm()).item()
     print(f"config 5 rel-L2 vs fp32 matmul of dequantized operands: {r:.3e}")
     assert r <= 4e-3
+    # and a slice against the CPU oracle end to end: 256 rows of A x 1024 rows of W
+    rows, cols = slice(0, 256), slice(0, 1024)
+
+    def rows_of(sc, n, sl):
+        return ref.to_blocked(ref.from_blocked(sc.cpu().view(torch.uint8), n, 5120 // 16)[sl].contiguous()).view(
+            torch.float8_e4m3fn)
+
+    want_cpu = ref.scaled_mm_nvfp4_ref(qa[rows].cpu(), qw[cols].cpu(), ga.cpu(), gw.cpu(), rows_of(sa, 8192, rows),
+                                       rows_of(sw, 13824, cols), out_dtype=torch.float32)
+    assert rel_l2(got[rows, cols], want_cpu) <= 4e-3
