@@ -122,7 +122,14 @@ struct Args {
     // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
     const float* tsa;
     const float* tsb;
+    // split-K mode (gemm_split_kernel): workgroup L * splits + s computes stages
+    // [s * ks, min((s + 1) * ks, KT)) of tile L and writes its fp32 partial tile to part
+    int splits, ks;
+    float* part;
 };
+
+// fp32 values of one partial tile in the workspace (256 x 256)
+constexpr int kPartTile = BM * BN;
 
 // Register-staged loads of one operand for a pair of stages (s, s + 1), i.e. K bytes
 // [k0, k0 + 128) of the tile's 256 (or 128) rows.  Wave w, load j (0..7, or 0..3)
@@ -282,17 +289,28 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
 // array and writes staged data into the other, so the compiler knows they never alias
 // and may interleave the two freely; within an array, per-lane addresses of different
 // buffers differ only by immediates.
-template <int OUT, int BIAS, bool UNIT, int NW>
+template <int OUT, int BIAS, bool UNIT, int NW, bool SPLIT = false>
 __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01, uint8_t* lds23) {
     constexpr int TBN = 64 * NW;  // tile width along n
     constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
     constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
+    static_assert(!SPLIT || NW == 4, "split-K runs full tiles");
 
     // Workgroups are dispatched round-robin over the 8 XCDs; full tiles are remapped so
     // each XCD walks a contiguous range of tiles (in grouped order).  Half tiles give
-    // tile L's two column halves to consecutive workgroups.
-    if (NW == 4 && (p.n_full & 7) == 0) bid = (bid & 7) * (p.n_full >> 3) + (bid >> 3);
-    const int L = NW == 4 ? bid : p.n_full + (bid >> 1);
+    // tile L's two column halves to consecutive workgroups.  Split-K workgroups take tile
+    // bid / splits, K range bid % splits.
+    const int KT = (p.K + BK - 1) / BK;
+    const int split = SPLIT ? bid % p.splits : 0;
+    if (SPLIT) bid /= p.splits;
+    else if (NW == 4 && (p.n_full & 7) == 0) bid = (bid & 7) * (p.n_full >> 3) + (bid >> 3);
+    // this workgroup's stages [t0, t1) (t0 a multiple of 4), the bytes of K they cover and
+    // the 128-wide scale blocks: loads past them read zeros
+    const int t0 = SPLIT ? split * p.ks : 0;
+    const int t1 = SPLIT ? min(t0 + p.ks, KT) : KT;
+    const int kend = SPLIT ? min(t1 * BK, p.K) : p.K;
+    const int pend = SPLIT ? min(p.ncb, (t1 + 1) / 2) : p.ncb;
+    const int L = (NW == 4) ? bid : p.n_full + (bid >> 1);
     int tm, tn;
     grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
@@ -311,7 +329,6 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const FragAddr fab = make_frag_addr(wn * 32 * NW, lane);
     const FragAddr faa = make_frag_addr(wm * 128, lane);
-    const int KT = (p.K + BK - 1) / BK;
 
     v16f acc[NW][4];
 #pragma unroll
@@ -325,7 +342,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     };
     // Register staging: a pair of stages of one operand at a time.
     v4u SB[8], SA[8];
-    auto load_b = [&](int s) { load_pair<PB>(LB, SB, s * BK, p.K); };
+    auto load_b = [&](int s) { load_pair<PB>(LB, SB, s * BK, kend); };
     // Scale words: a lane's 4 words for its wave's 4 32-row tiles of an operand and one
     // 128-wide K block (pair of stages) are 16 contiguous bytes of the swizzled tensor, at
     // chunk ((row128 / 128) * ncb + pair) * 512 + r32 * 16 for the tiles' 128-row block
@@ -336,11 +353,11 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     const uint32_t dsa_off = static_cast<uint32_t>(((m0 >> 7) + wm) * p.ncb * 512 + r32 * 16);
     v4u DWB, DWA;  // words of the next pair not yet consumed
     auto load_dscales = [&](int pair) {
-        const uint32_t po = pair < p.ncb ? static_cast<uint32_t>(pair * 512) : 0x80000000u;
+        const uint32_t po = pair < pend ? static_cast<uint32_t>(pair * 512) : 0x80000000u;
         DWB = __builtin_amdgcn_raw_buffer_load_b128(rssb, dsb_off + po, 0, 0);
         DWA = __builtin_amdgcn_raw_buffer_load_b128(rssa, dsa_off + po, 0, 0);
     };
-    auto load_a = [&](int s) { load_pair(LA, SA, s * BK, p.K); };
+    auto load_a = [&](int s) { load_pair(LA, SA, s * BK, kend); };
     auto store_a = [&](auto x_c, auto y_c) { store_pair(LA, SA, buf(x_c) + TILE, buf(y_c) + TILE); };
     // this lane's 4 scale words (tiles t = 0..3) of each operand for a stage, shifted so
     // byte 0 / byte 2 are the lane-half's scales of the even / odd 64-wide stage
@@ -377,7 +394,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
         const uint8_t* nx = buf(Next{});
         uint8_t* wx = EVEN ? buf(P2{}) : buf(P3{}) + TILE;
         uint8_t* wy = EVEN ? buf(P3{}) : buf(b_c) + TILE;
-        const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, p.K) : pair_add(LB, (t + 3) * BK, p.K);
+        const uint32_t add = EVEN ? pair_add(LA, (t + 4) * BK, kend) : pair_add(LB, (t + 3) * BK, kend);
         uint32_t nb[4], na[4];
         if constexpr (UNIT) {
 #pragma unroll
@@ -435,11 +452,11 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     // write, so the prologue waits out one memory latency rather than two.
     {
         v4u XA[8], XB[8];
-        load_a(0);
-        load_pair<PB>(LB, XB, 0, p.K);
-        if constexpr (DS) load_dscales(0);
-        load_pair(LA, XA, 2 * BK, p.K);
-        load_b(2);
+        load_a(t0);
+        load_pair<PB>(LB, XB, t0 * BK, kend);
+        if constexpr (DS) load_dscales(t0 / 2);
+        load_pair(LA, XA, (t0 + 2) * BK, kend);
+        load_b(t0 + 2);
         store_a(B0{}, B1{});
         store_pair<PB>(LB, XB, buf(B0{}), buf(B1{}));
         store_pair(LA, XA, buf(B2{}) + TILE, buf(B3{}) + TILE);
@@ -452,18 +469,36 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
             scb[u] = (NW == 4 ? DWB[u] : (sbt ? DWB[2 + (u & 1)] : DWB[u & 1])) >> hs;
             sca[u] = DWA[u] >> hs;
         }
-        load_dscales(1);
+        load_dscales(t0 / 2 + 1);
     } else {
 #pragma unroll
         for (int u = 0; u < 4; ++u) scb[u] = sca[u] = 0x7f7f7f7fu;
     }
 
     // stages in groups of 4 (buffer index = stage % 4); stages past K are all zeros
-    for (int t = 0; t < KT; t += 4) {
+    for (int t = t0; t < t1; t += 4) {
         stage(B0{}, t, F0, F1);
         stage(B1{}, t + 1, F1, F0);
         stage(B2{}, t + 2, F0, F1);
         stage(B3{}, t + 3, F1, F0);
+    }
+    if constexpr (SPLIT) {
+        __builtin_amdgcn_s_waitcnt(0);  // prefetches past this range (zeros) have landed
+        // The raw fp32 accumulators go to the workspace in register order: float4 g of
+        // MFMA tile (i, j) of wave w, lane l at ((w * 16 + 4 i + j) * 4 + g) * 64 + l, so
+        // every store instruction writes 1 KB contiguously.  The reduce kernel adds the
+        // splits and runs the epilogue.
+        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPartTile / 4) +
+                      wave * 4096 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    dst[((4 * i + j) * 4 + g) * 64] =
+                        make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        return;
     }
     // the epilogue reuses the LDS buffers
     __syncthreads();
@@ -561,6 +596,60 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     const int b = blockIdx.x;
     if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4>(p, b, lds01, lds23);
     else gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
+}
+
+// Split-K, first launch: each workgroup one K range of one 256 x 256 tile, partial sums to
+// the workspace (no output, bias or tensor scale here).
+template <bool UNIT>
+__global__ __launch_bounds__(NT) void gemm_split_kernel(Args p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
+    gemm_tile<CKH_F32, -1, UNIT, 4, true>(p, blockIdx.x, lds01, lds23);
+}
+
+// Split-K, second launch: thread q adds float4 q % 16384 of tile q / 16384 over the splits
+// in split order (the sum does not depend on which workgroup finished first), then applies
+// the tensor scale and bias and stores out[m][n .. n + 3] (the register mapping of the tile
+// kernel's epilogue).
+template <int OUT, int BIAS, bool UNIT>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int L = static_cast<int>(q >> 14);
+    if (L >= p.tiles_m * p.tiles_n) return;
+    const int rest = static_cast<int>(q & 16383);
+    const int wave = rest >> 12, ij = (rest >> 8) & 15, g = (rest >> 6) & 3, lane = rest & 63;
+    const int i = ij >> 2, j = ij & 3;
+    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(L) * p.splits * (kPartTile / 4) + rest;
+    float4 v = src[0];
+    for (int s = 1; s < p.splits; ++s) {
+        const float4 w = src[static_cast<int64_t>(s) * (kPartTile / 4)];
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    }
+    int tm, tn;
+    grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
+    const int m = tm * BM + (wave & 1) * 128 + j * 32 + (lane & 31);
+    const int n = tn * BN + (wave >> 1) * 128 + i * 32 + 8 * g + 4 * (lane >> 5);
+    if (m >= p.M || n >= p.N) return;
+    float o[4] = {v.x, v.y, v.z, v.w};
+    const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (UNIT) o[e] *= alpha;
+        if constexpr (BIAS >= 0) o[e] += n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f;
+        // kept from being fused with the narrowing into one mixed-precision rounding
+        if constexpr (UNIT || BIAS >= 0) o[e] = opaque(o[e]);
+    }
+    const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+    if (n + 3 < p.N && (p.N & 3) == 0) {
+        store4<OUT>(p.out, idx, o);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) store1<OUT>(p.out, idx + e, o[e]);
+    }
 }
 
 }  // namespace mx
@@ -861,14 +950,81 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
     return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }
 
+// Split-K: a grid of at most half as many 256 x 256 tiles as CUs leaves most CUs idle
+// while each tile walks all of K.  Such a grid with long K instead runs S K ranges of every
+// tile (each of ks stages, a multiple of 4, at least kMinSplitStages) as S times as many
+// workgroups, at most one per CU, which write fp32 partial tiles to the caller's workspace;
+// a second launch adds them.  A partial tile (256 KB) costs about as much memory traffic
+// to write and again to read back as 8 stages of operand loads, so short K (fewer than
+// kMinSplitK stages) keeps whole-K half tiles instead.  Measured, graph-timed: M = 256,
+// N = 5120, K = 13824 40.5 against 110.8 us (half tiles); N = 13824, K = 5120 40.1 against
+// 46.9 us; N = 18432, K = 3072 38.3 against 32.1 us (not split).  Returns S (1: no split)
+// and sets ks.
+constexpr int kMinSplitStages = 12;
+constexpr int kMinSplitK = 64;  // stages
+
+int split_count(int M, int N, int K, int& ks) {
+    ks = 0;
+    if (M <= kSkinnyMaxM) return 1;
+    const int tiles = static_cast<int>(cdiv(M, mx::BM) * cdiv(N, mx::BN));
+    const int KT = static_cast<int>(cdiv(K, mx::BK));
+    if (tiles > kGemmSlots / 2 || KT < kMinSplitK) return 1;
+    const int S = min(kGemmSlots / tiles, KT / kMinSplitStages);
+    if (S < 2) return 1;
+    ks = static_cast<int>(rup(cdiv(KT, S), 4));
+    return static_cast<int>(cdiv(KT, ks));
+}
+
+int64_t split_workspace_bytes(int M, int N, int K) {
+    int ks;
+    const int S = split_count(M, N, K, ks);
+    if (S < 2) return 0;
+    return cdiv(M, mx::BM) * cdiv(N, mx::BN) * S * static_cast<int64_t>(mx::kPartTile) * 4;
+}
+
+template <bool UNIT>
+void launch_split(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    const int tiles = p.tiles_m * p.tiles_n;
+    hipLaunchKernelGGL((mx::gemm_split_kernel<UNIT>), dim3(static_cast<unsigned>(tiles * p.splits)), dim3(mx::NT), 0,
+                       st, p);
+    const dim3 g2(static_cast<unsigned>(tiles * (mx::kPartTile / 4 / 256)));
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_reduce_kernel<O, B, UNIT>), g2, dim3(256), 0, st, p)
+#define BY_BIAS(O)                                                     \
+    do {                                                               \
+        if (!has_bias) LAUNCH(O, -1);                                  \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32);             \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16);             \
+        else LAUNCH(O, CKH_BF16);                                      \
+    } while (0)
+    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+    else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef LAUNCH
+}
+
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
 // half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
-// half tiles (about 55% of a full tile's time each), in the same grid.
+// half tiles (about 55% of a full tile's time each), in the same grid.  Activations of at
+// most kSkinnyMaxM rows take the skinny kernel, and small grids split K when the caller
+// gives a workspace.
 template <bool UNIT>
-int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, void* workspace, int64_t workspace_bytes,
+                hipStream_t st) {
     if (p.M <= kSkinnyMaxM) return launch_skinny<UNIT>(p, out_code, bias_code, has_bias, st);
+    int ks;
+    const int S = split_count(p.M, p.N, p.K, ks);
+    if (S > 1 && workspace && workspace_bytes >= split_workspace_bytes(p.M, p.N, p.K)) {
+        p.splits = S;
+        p.ks = ks;
+        p.part = static_cast<float*>(workspace);
+        launch_split<UNIT>(p, out_code, bias_code, has_bias, st);
+        return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
+    }
     const int tiles = p.tiles_m * p.tiles_n;
-    const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : 0;
+    // (a grid of at most half as many tiles as CUs with no workspace for split-K runs all
+    // of its tiles as half tiles: 256 x 18432 x 3072 measured 31.9 against 41.3 us)
+    const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : tiles;
     p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
     p.n_full = tiles - p.n_half;
     launch_grid<UNIT>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
@@ -891,9 +1047,14 @@ mx::Args base_args(const void* a, const void* b, const void* bias, void* out, in
 
 }  // namespace
 
+extern "C" int64_t ckh_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 24)) return 0;
+    return split_workspace_bytes(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K));
+}
+
 extern "C" int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa, const void* sb, const void* bias,
                                    void* out, int64_t M, int64_t N, int64_t K, int out_code, int bias_code,
-                                   uintptr_t stream) {
+                                   void* workspace, int64_t workspace_bytes, uintptr_t stream) {
     CKH_REQUIRE(a && b && sa && sb && out, "scaled_mm_mxfp8: null pointer");
     CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_mxfp8: sizes must be M, N >= 0 and K > 0");
     CKH_REQUIRE(K % 32 == 0, "scaled_mm_mxfp8: K (%lld) must be a multiple of 32", (long long)K);
@@ -912,12 +1073,14 @@ extern "C" int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa,
     p.ncb = static_cast<int>(cdiv(K / 32, 4));
     p.sa_rows = static_cast<int>(rup(M, 128));
     p.sb_rows = static_cast<int>(rup(N, 128));
-    return launch_gemm<false>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
+    CKH_REQUIRE(!workspace || aligned(workspace, 16), "scaled_mm_mxfp8: workspace misaligned");
+    return launch_gemm<false>(p, out_code, bias_code, bias != nullptr, workspace, workspace_bytes,
+                              reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const float* scale_b,
                                  const void* bias, void* out, int64_t M, int64_t N, int64_t K, int out_code,
-                                 int bias_code, uintptr_t stream) {
+                                 int bias_code, void* workspace, int64_t workspace_bytes, uintptr_t stream) {
     CKH_REQUIRE(a && b && scale_a && scale_b && out, "scaled_mm_fp8: null pointer");
     CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_fp8: sizes must be M, N >= 0 and K > 0");
     CKH_REQUIRE(K % 16 == 0, "scaled_mm_fp8: K (%lld) must be a multiple of 16", (long long)K);
@@ -933,5 +1096,7 @@ extern "C" int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scal
     mx::Args p = base_args(a, b, bias, out, M, N, K);
     p.tsa = scale_a;
     p.tsb = scale_b;
-    return launch_gemm<true>(p, out_code, bias_code, bias != nullptr, reinterpret_cast<hipStream_t>(stream));
+    CKH_REQUIRE(!workspace || aligned(workspace, 16), "scaled_mm_fp8: workspace misaligned");
+    return launch_gemm<true>(p, out_code, bias_code, bias != nullptr, workspace, workspace_bytes,
+                             reinterpret_cast<hipStream_t>(stream));
 }

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CKH_ABI_VERSION 7
+#define CKH_ABI_VERSION 8
 
 enum ckh_dtype {
     CKH_F32 = 0,
@@ -140,27 +140,44 @@ int ckh_apply_rope(const void* xq, const void* xk, const void* freqs, void* xq_o
                    int freqs_code, uintptr_t stream);
 
 /*
+ * Bytes of device workspace ckh_scaled_mm_mxfp8 / ckh_scaled_mm_fp8 use at this shape to
+ * split K (0: the shape does not split).  A grid of at most 128 output tiles of 256 x 256
+ * (e.g. M = 256, N = 18432) splits K over up to 256 workgroups, which write fp32 partial
+ * tiles (256 KB each) to the workspace; a second launch adds them in a fixed order and
+ * applies scale, bias and output rounding.  No counterpart in the reference (torch's
+ * scaled_mm takes no workspace).
+ */
+int64_t ckh_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
  * MXFP8 GEMM: out[M,N] = sum_k A[m,k]*2^(sa-127) * B[n,k]*2^(sb-127) (+ bias[n]).
  * a [M,K] e4m3, b [N,K] e4m3 (both K-major), sa/sb E8M0 swizzled with logical shapes
  * [M, K/32] / [N, K/32]; bias NULL or [N] of bias_code (f32/f16/bf16);
  * out [M,N] row-major of out_code (f32/f16/bf16).  K % 32 == 0.
+ * workspace: NULL, or ckh_scaled_mm_workspace_bytes(M, N, K) bytes of device memory
+ * (16-byte aligned) that the call may overwrite; with less than that the call does not
+ * split K (same result within fp32 summation order, slower on small grids).  Calls running
+ * at the same time need workspaces of their own.
  * No native counterpart in the reference (eager quantization.py:367-402 routes to
  * torch F.scaled_mm via scaled_mm_v2.py:27-53); replaces that call.
  */
 int ckh_scaled_mm_mxfp8(const void* a, const void* b, const void* sa, const void* sb,
                         const void* bias, void* out, int64_t M, int64_t N, int64_t K,
-                        int out_code, int bias_code, uintptr_t stream);
+                        int out_code, int bias_code, void* workspace, int64_t workspace_bytes,
+                        uintptr_t stream);
 
 /*
  * Per-tensor FP8 GEMM: out[M,N] = scale_a * scale_b * sum_k A[m,k] * B[n,k] (+ bias[n]).
  * a [M,K] e4m3, b [N,K] e4m3 (both K-major), scale_a / scale_b one f32 each on device;
  * bias NULL or [N] of bias_code; out [M,N] row-major of out_code.  K % 16 == 0.
+ * workspace: as for ckh_scaled_mm_mxfp8.
  * Replaces the TensorWise torch F.scaled_mm call behind TensorCoreFP8Layout's
  * linear / mm / addmm (tensor/fp8.py:86-101 -> scaled_mm_v2.py:27-53).
  */
 int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const float* scale_b,
                       const void* bias, void* out, int64_t M, int64_t N, int64_t K,
-                      int out_code, int bias_code, uintptr_t stream);
+                      int out_code, int bias_code, void* workspace, int64_t workspace_bytes,
+                      uintptr_t stream);
 
 /*
  * NVFP4 GEMM: out[M,N] = alpha * sum_k E2M1(a)*sa[m,k/16] * E2M1(b)*sb[n,k/16] (+bias[n]).

@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.ckh_abi_version() == hb.ABI_VERSION == 7
+    assert lib.ckh_abi_version() == hb.ABI_VERSION == 8
 
 
 def test_amax_workspace_size_matches_header():

@@ -142,6 +142,74 @@ def test_scaled_mm_skinny_bias_and_per_tensor(bias_dtype, m, hip):
         assert rel_l2(got, want) <= REL_L2[out_dtype]
 
 
+def _mx_abi(qx, qw, sx, sw, out_dtype, ws):
+    """ckh_scaled_mm_mxfp8 through the C ABI with an explicit workspace (None: no split)."""
+    import comfy_kitchen.backends.hip as hb
+
+    m, k = qx.shape
+    n = qw.shape[0]
+    out = torch.empty(m, n, dtype=out_dtype, device="cuda")
+    hb._call("ckh_scaled_mm_mxfp8", qx.data_ptr(), qw.data_ptr(), sx.data_ptr(), sw.data_ptr(), None, out.data_ptr(),
+             m, n, k, hb.DTYPE_TO_CODE[out_dtype], 0, None if ws is None else ws.data_ptr(),
+             0 if ws is None else ws.numel(), torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(256, 4096, 4096), (300, 2000, 4160), (129, 520, 4128), (65, 18432, 4096),
+                                   (512, 3072, 13824)])
+def test_scaled_mm_mxfp8_split_k(m, n, k, out_dtype, hip):
+    """Grids of at most 128 tiles split K over more workgroups into a workspace, and a second
+    launch adds the partial tiles (fixed order) and runs the epilogue: against the oracle,
+    and against the same call with no workspace (whole-K half tiles), which differs only in
+    fp32 summation order.  Covers a last K range shorter than the others (and than one
+    group of 4 stages), K % 64 == 32, rows past M and columns past N."""
+    import comfy_kitchen.backends.hip as hb
+
+    nbytes = hb._lib.ckh_scaled_mm_workspace_bytes(m, n, k)
+    assert nbytes > 0
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=m + 5 * n + k)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, out_dtype=torch.float32)
+    qx, sx, qw, sw = qx.cuda(), sx.cuda(), qw.cuda(), sw.cuda()
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN garbage: every byte is rewritten
+    got = _mx_abi(qx, qw, sx, sw, out_dtype, ws)
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+    assert torch.equal(got, _mx_abi(qx, qw, sx, sw, out_dtype, ws))  # deterministic
+    whole = _mx_abi(qx, qw, sx, sw, out_dtype, None)
+    if out_dtype == torch.float32:
+        assert rel_l2(got, whole) <= 1e-6
+    assert torch.equal(ck.scaled_mm_mxfp8(qx, qw, sx, sw, out_dtype=out_dtype), got)  # the wrapper splits too
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32])
+def test_scaled_mm_split_k_bias_and_per_tensor(bias_dtype, hip):
+    """The split-K reduce kernel's epilogue: bias, and the per-tensor FP8 mode."""
+    m, n, k = 200, 1000, 4096
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=31)
+    bias = (torch.randn(n) * 2).to(bias_dtype)
+    want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), bias=bias.cuda(), out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+    ta, tb = torch.tensor([0.37]), torch.tensor([1.9e-3])
+    want = (qx.float() @ qw.float().t()) * (ta * tb) + bias.float()
+    for out_dtype in (torch.float32, torch.bfloat16):
+        got = ck.scaled_mm_fp8(qx.cuda(), qw.cuda(), ta.cuda(), tb.cuda(), bias=bias.cuda(), out_dtype=out_dtype)
+        assert rel_l2(got, want) <= REL_L2[out_dtype]
+
+
+def test_scaled_mm_workspace_bytes(hip):
+    """Only small tile grids with enough K split; big grids, skinny M and short K do not."""
+    import comfy_kitchen.backends.hip as hb
+
+    f = hb._lib.ckh_scaled_mm_workspace_bytes
+    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 80 stages: 4 ranges of 20
+    assert f(256, 5120, 13824) == 20 * 11 * 256 * 256 * 4  # 216 stages: 11 ranges of 20
+    assert f(4608, 12288, 13824) == 0  # 864 tiles
+    assert f(64, 18432, 13824) == 0  # skinny kernel
+    assert f(256, 18432, 3072) == 0  # 48 stages: whole-K half tiles
+    assert f(0, 4096, 8192) == 0 and f(256, 4096, -1) == 0
+
+
 def test_scaled_mm_mxfp8_rejects_bad_shapes(hip):
     a = torch.zeros(64, 96, dtype=torch.float8_e4m3fn, device="cuda")
     b = torch.zeros(64, 64, dtype=torch.float8_e4m3fn, device="cuda")
