@@ -59,7 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "ckh_scaled_mm_workspace_bytes": (_i64, [_i64] * 3),
     "ckh_scaled_mm_mxfp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _p, _i64, _u64]),
     "ckh_scaled_mm_fp8": (_i32, [_p] * 6 + [_i64] * 3 + [_i32, _i32, _p, _i64, _u64]),
-    "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _u64]),
+    "ckh_scaled_mm_nvfp4": (_i32, [_p] * 7 + [_i64] * 3 + [_i32, _i32, _p, _i64, _u64]),
+    "ckh_scaled_mm_nvfp4_workspace_bytes": (_i64, [_i64] * 3),
     "ckh_amax_scale": (_i32, [_p, _i64, _i32, _f32, _p, _p, _u64]),
     "ckh_amax_scale_noalloc": (_i32, [_p, _i64, _i32, _f32, _p, _u64]),
     "ckh_quantize_nvfp4_dynamic": (_i32, [_p, _f32, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _p, _u64]),
@@ -298,14 +299,15 @@ def _bias_args(bias: torch.Tensor | None, n: int, device) -> tuple[torch.Tensor 
 
 
 @functools.lru_cache(maxsize=256)
-def _split_workspace_bytes(m: int, n: int, k: int) -> int:
-    return int(_lib.ckh_scaled_mm_workspace_bytes(m, n, k))
+def _split_workspace_bytes(fn: str, m: int, n: int, k: int) -> int:
+    return int(getattr(_lib, fn)(m, n, k))
 
 
-def _gemm_workspace(m: int, n: int, k: int, device: torch.device) -> tuple[torch.Tensor | None, int]:
-    """The workspace the MXFP8 / FP8 GEMM splits K in at this shape (small tile grids), from
-    torch's allocator (graph-capture safe), or (None, 0)."""
-    nbytes = _split_workspace_bytes(m, n, k)
+def _gemm_workspace(m: int, n: int, k: int, device: torch.device,
+                    fn: str = "ckh_scaled_mm_workspace_bytes") -> tuple[torch.Tensor | None, int]:
+    """The workspace a GEMM splits K in at this shape (small tile grids), from torch's
+    allocator (graph-capture safe), or (None, 0)."""
+    nbytes = _split_workspace_bytes(fn, m, n, k)
     if nbytes <= 0:
         return None, 0
     return torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
@@ -378,9 +380,11 @@ def scaled_mm_nvfp4(a: torch.Tensor, b: torch.Tensor, tensor_scale_a: torch.Tens
             raise ValueError(f"scaled_mm_nvfp4: {name} has {s.numel()} bytes, needs {need}")
     bias_t, bias_code = _bias_args(bias, n, a.device)
     out = torch.empty((m, n), dtype=out_dtype, device=a.device)
+    ws, ws_bytes = _gemm_workspace(m, n, k, a.device, "ckh_scaled_mm_nvfp4_workspace_bytes")
     with _on_device(a):
         _call("ckh_scaled_mm_nvfp4", a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), alpha.data_ptr(),
-              _ptr(bias_t), out.data_ptr(), m, n, k, DTYPE_TO_CODE[out_dtype], bias_code, _stream(a))
+              _ptr(bias_t), out.data_ptr(), m, n, k, DTYPE_TO_CODE[out_dtype], bias_code, _ptr(ws), ws_bytes,
+              _stream(a))
     return out
 
 

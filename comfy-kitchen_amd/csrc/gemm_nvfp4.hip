@@ -97,7 +97,14 @@ struct Args {
     int ncb;      // scale word columns: ceil(K/16/4)
     int sa_rows, sb_rows;
     int tiles_m, tiles_n;
+    // split-K mode (gemm_split_kernel): workgroup L * splits + s computes groups
+    // [s * ks, min((s + 1) * ks, NG)) of tile L (ks even) and writes its fp32 partial tile
+    int splits, ks;
+    float* part;
 };
+
+// fp32 values of one partial tile in the workspace (256 x 256)
+constexpr int kPartTile = BM * BN;
 
 // Direct-to-LDS loads of one operand's group.  Wave w, load j (0..7) covers rows
 // R = 64 w + 8 j .. +7 (1 KB of LDS); lane i fills row R + i/8, physical chunk i%8,
@@ -138,11 +145,12 @@ __device__ __forceinline__ void issue_codes(const Loader& L, uint8_t* dst, int w
 // Scale words of a group: for a 256-row tile, 128-row block rb and word column c, the
 // 512-byte chunk ((rb0 + rb) * ncb + c) of the swizzled tensor; the 4 columns of a group
 // are contiguous, so each block's group is one 2 KB run.  Wave w copies block rb = w & 1
-// of operand w >> 1 (0 = weight, 1 = activation): 2 loads of 1 KB.  Columns past the
-// last (ncb) and blocks past the padded rows arrive as zeros.  Inside a chunk row r's
+// of operand w >> 1 (0 = weight, 1 = activation): 2 loads of 1 KB.  Columns from cend on
+// (the last, or the end of a split's K range) and blocks past the padded rows arrive as
+// zeros.  Inside a chunk row r's
 // word sits at (r % 32) * 16 + ((r % 128) / 32) * 4.
 __device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdgpu_buffer_rsrc_t rs_a, int rb0_b,
-                                             int rb0_a, int ncb, int g, uint8_t* sdst, int wave, int lane,
+                                             int rb0_a, int ncb, int cend, int g, uint8_t* sdst, int wave, int lane,
                                              int q0 = 0, int q1 = 2) {
     const int op = wave >> 1, rb = wave & 1;
     const __amdgpu_buffer_rsrc_t rs = op ? rs_a : rs_b;
@@ -151,7 +159,7 @@ __device__ __forceinline__ void issue_scales(__amdgpu_buffer_rsrc_t rs_b, __amdg
     for (int q = q0; q < q1; ++q) {
         const int col = GS * g + 2 * q + (lane >> 5);
         const uint32_t off =
-            col < ncb ? static_cast<uint32_t>((base * ncb + col) * 512 + (lane & 31) * 16) : 0x80000000u;
+            col < cend ? static_cast<uint32_t>((base * ncb + col) * 512 + (lane & 31) * 16) : 0x80000000u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(sdst + op * STILE + rb * 2048 + q * 1024), 16, off,
                                                  0, 0, 0);
     }
@@ -197,14 +205,13 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
     else return load1<BIAS>(bias, n);
 }
 
-template <int OUT, int BIAS>
-__global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
-
+template <int OUT, int BIAS, bool SPLIT = false>
+__device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t* lds1) {
     const int tiles = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
-    if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+    const int split = SPLIT ? bid % p.splits : 0;
+    if (SPLIT) bid /= p.splits;
+    else if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
     int tm, tn;
     grouped_tile(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
@@ -221,6 +228,12 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const int NG = (Kb + GKB - 1) / GKB;  // groups of 256 elements
+    // this workgroup's groups [gb, ge) (gb even), the code bytes and scale-word columns they
+    // cover: loads past them read zeros
+    const int gb = SPLIT ? split * p.ks : 0;
+    const int ge = SPLIT ? min(gb + p.ks, NG) : NG;
+    const int kend = SPLIT ? min(ge * GKB, Kb) : Kb;
+    const int cend = SPLIT ? min(p.ncb, ge * GS) : p.ncb;
 
     v16f acc[4][4];
 #pragma unroll
@@ -231,17 +244,17 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     auto gbuf = [&](auto g_c) -> uint8_t* { return (decltype(g_c)::value & 1) ? lds1 : lds0; };
     auto issue_group = [&](auto g_c, int g) {
         uint8_t* d = gbuf(g_c);
-        issue_codes(LB, d, wave, g * GKB, Kb);
-        issue_codes(LA, d + TILE, wave, g * GKB, Kb);
-        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, g, d + 2 * TILE, wave, lane);
+        issue_codes(LB, d, wave, g * GKB, kend);
+        issue_codes(LA, d + TILE, wave, g * GKB, kend);
+        issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, cend, g, d + 2 * TILE, wave, lane);
     };
     // load I (0..17) of issue_group: weight codes 0..7, activation codes 8..15, scales 16, 17
     auto issue_part = [&](auto g_c, int g, auto i_c) {
         constexpr int I = decltype(i_c)::value;
         uint8_t* d = gbuf(g_c);
-        if constexpr (I < 8) issue_code_part(LB, d, wave, g * GKB, Kb, I);
-        else if constexpr (I < 16) issue_code_part(LA, d + TILE, wave, g * GKB, Kb, I - 8);
-        else issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, g, d + 2 * TILE, wave, lane, I - 16, I - 15);
+        if constexpr (I < 8) issue_code_part(LB, d, wave, g * GKB, kend, I);
+        else if constexpr (I < 16) issue_code_part(LA, d + TILE, wave, g * GKB, kend, I - 8);
+        else issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, cend, g, d + 2 * TILE, wave, lane, I - 16, I - 15);
     };
 
     // lane's fragment and scale-word addresses inside a group buffer
@@ -331,14 +344,14 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     };
 
     // prologue: groups 0 and 1 in flight, group 0 resident, stage 0 read and decoded
-    issue_group(G0{}, 0);
-    issue_group(G1{}, 1);
+    issue_group(G0{}, gb);
+    issue_group(G1{}, gb + 1);
     group_barrier<waitcnt_vm_lgkm0(LOADS_PER_GROUP)>();
     for_each_index([&](auto i_c) { read_part(lds0, S0{}, i_c, R0); }, std::make_integer_sequence<int, 10>{});
     for_each_index([&](auto p_c) { decode_part(R0, K0{}, p_c, D0); }, std::make_integer_sequence<int, 16>{});
 
     // groups in pairs (buffer = group % 2); groups past K are all zeros
-    for (int g = 0; g < NG; g += 2) {
+    for (int g = gb; g < ge; g += 2) {
         stage(G0{}, S0{}, g, R0, R1);
         stage(G0{}, S1{}, g, R1, R0);
         stage(G0{}, S2{}, g, R0, R1);
@@ -350,6 +363,23 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     }
     // the loads of the groups past the end still write LDS, which the epilogue reuses
     __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (SPLIT) {
+        // The raw fp32 accumulators go to the workspace in register order: float4 g of
+        // MFMA tile (i, j) of wave w, lane l at ((w * 16 + 4 i + j) * 4 + g) * 64 + l, so
+        // every store instruction writes 1 KB contiguously.  The reduce kernel adds the
+        // splits and runs the epilogue.
+        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPartTile / 4) +
+                      wave * 4096 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    dst[((4 * i + j) * 4 + g) * 64] =
+                        make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        return;
+    }
     __syncthreads();
 
     // Epilogue: lane holds out[m][n..n+3] for m = r32-th row of activation tile j and
@@ -418,6 +448,61 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
                 }
             }
         }
+    }
+}
+
+template <int OUT, int BIAS>
+__global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
+    gemm_tile<OUT, BIAS>(p, lds0, lds1);
+}
+
+// Split-K, first launch: each workgroup one K range of one tile, partial sums to the
+// workspace (alpha and bias are applied by the reduce kernel).
+__global__ __launch_bounds__(NT) void gemm_split_kernel(Args p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
+    gemm_tile<CKH_F32, -1, true>(p, lds0, lds1);
+}
+
+// Split-K, second launch: thread q adds float4 q % 16384 of tile q / 16384 over the splits
+// in split order, times alpha, plus bias, and stores out[m][n .. n + 3] (the register
+// mapping of the tile epilogue).
+template <int OUT, int BIAS>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int L = static_cast<int>(q >> 14);
+    if (L >= p.tiles_m * p.tiles_n) return;
+    const int rest = static_cast<int>(q & 16383);
+    const int wave = rest >> 12, ij = (rest >> 8) & 15, g = (rest >> 6) & 3, lane = rest & 63;
+    const int i = ij >> 2, j = ij & 3;
+    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(L) * p.splits * (kPartTile / 4) + rest;
+    float4 v = src[0];
+    for (int s = 1; s < p.splits; ++s) {
+        const float4 w = src[static_cast<int64_t>(s) * (kPartTile / 4)];
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    }
+    int tm, tn;
+    grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
+    const int m = tm * BM + (wave & 1) * 128 + j * 32 + (lane & 31);
+    const int n = tn * BN + (wave >> 1) * 128 + i * 32 + 8 * g + 4 * (lane >> 5);
+    if (m >= p.M || n >= p.N) return;
+    const float alpha = p.alpha[0];
+    const float s4[4] = {v.x, v.y, v.z, v.w};
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = s4[e] * alpha + (n + e < p.N ? bias_at<BIAS>(p.bias, n + e) : 0.0f);
+    const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+    if (n + 3 < p.N && (p.N & 3) == 0) {
+        store4<OUT>(p.out, idx, o);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < p.N) store1<OUT>(p.out, idx + e, o[e]);
     }
 }
 
@@ -785,6 +870,35 @@ namespace {
 // Activations of at most kNvSkinnyMaxM rows take the skinny kernel (nvsk::gemm_skinny_kernel).
 constexpr int kNvSkinnyMaxM = 64;
 
+// Split-K: a grid of at most 128 tiles (half the CUs) with at least kNvMinSplitK groups of
+// 256 elements runs S K ranges of every tile (each an even number of groups, at least
+// kNvMinSplitGroups) as S times as many workgroups, at most 256, which write fp32 partial
+// tiles to the caller's workspace; a second launch adds them.  A group costs about 4 us of
+// MFMA time per tile and a partial tile's round trip about as much as one group.  Returns
+// S (1: no split) and sets ks.
+constexpr int kNvSlots = 256;
+constexpr int kNvMinSplitK = 8;
+constexpr int kNvMinSplitGroups = 4;
+
+int nv_split_count(int64_t M, int64_t N, int64_t K, int& ks) {
+    ks = 0;
+    if (M <= kNvSkinnyMaxM) return 1;
+    const int tiles = static_cast<int>(cdiv(M, nv::BM) * cdiv(N, nv::BN));
+    const int NG = static_cast<int>(cdiv(K / 2, nv::GKB));
+    if (tiles > kNvSlots / 2 || NG < kNvMinSplitK) return 1;
+    const int S = min(kNvSlots / tiles, NG / kNvMinSplitGroups);
+    if (S < 2) return 1;
+    ks = static_cast<int>(rup(cdiv(NG, S), 2));
+    return static_cast<int>(cdiv(NG, ks));
+}
+
+int64_t nv_split_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    int ks;
+    const int S = nv_split_count(M, N, K, ks);
+    if (S < 2) return 0;
+    return cdiv(M, nv::BM) * cdiv(N, nv::BN) * S * static_cast<int64_t>(nv::kPartTile) * 4;
+}
+
 int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bias, hipStream_t st) {
     nvsk::Args p{};
     p.a = q.a; p.b = q.b; p.sa = q.sa; p.sb = q.sb; p.alpha = q.alpha; p.bias = q.bias; p.out = q.out;
@@ -827,9 +941,14 @@ int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bi
 
 }  // namespace
 
+extern "C" int64_t ckh_scaled_mm_nvfp4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || M >= (1ll << 30) || N >= (1ll << 30) || K >= (1ll << 31)) return 0;
+    return nv_split_workspace_bytes(M, N, K);
+}
+
 extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void* sb, const void* alpha,
                                    const void* bias, void* out, int64_t M, int64_t N, int64_t K, int out_code,
-                                   int bias_code, uintptr_t stream) {
+                                   int bias_code, void* workspace, int64_t workspace_bytes, uintptr_t stream) {
     CKH_REQUIRE(a && b && sa && sb && alpha && out, "scaled_mm_nvfp4: null pointer");
     CKH_REQUIRE(M >= 0 && N >= 0 && K > 0, "scaled_mm_nvfp4: sizes must be M, N >= 0 and K > 0");
     CKH_REQUIRE(K % 32 == 0, "scaled_mm_nvfp4: K (%lld) must be a multiple of 32", (long long)K);
@@ -840,7 +959,7 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
     CKH_REQUIRE(!bias || bias_code == CKH_F32 || bias_code == CKH_F16 || bias_code == CKH_BF16,
                 "scaled_mm_nvfp4: unsupported bias dtype code %d", bias_code);
     CKH_REQUIRE(aligned(a, 16) && aligned(b, 16) && aligned(sa, 16) && aligned(sb, 16) && aligned(out, 16) &&
-                    aligned(alpha, 4),
+                    aligned(alpha, 4) && (!workspace || aligned(workspace, 16)),
                 "scaled_mm_nvfp4: pointers misaligned");
     if (M == 0 || N == 0) return CKH_OK;
     nv::Args p{};
@@ -861,6 +980,30 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
     p.tiles_n = static_cast<int>(cdiv(N, nv::BN));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (p.M <= kNvSkinnyMaxM) return launch_nv_skinny(p, out_code, bias_code, bias != nullptr, st);
+    int ks;
+    const int S = nv_split_count(M, N, K, ks);
+    if (S > 1 && workspace && workspace_bytes >= nv_split_workspace_bytes(M, N, K)) {
+        p.splits = S;
+        p.ks = ks;
+        p.part = static_cast<float*>(workspace);
+        const int tiles = p.tiles_m * p.tiles_n;
+        hipLaunchKernelGGL(nv::gemm_split_kernel, dim3(static_cast<unsigned>(tiles * S)), dim3(nv::NT), 0, st, p);
+        const dim3 g2(static_cast<unsigned>(tiles * (nv::kPartTile / 4 / 256)));
+#define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_reduce_kernel<O, B>), g2, dim3(256), 0, st, p)
+#define BY_BIAS(O)                                         \
+    do {                                                   \
+        if (!bias) LAUNCH(O, -1);                          \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
+        else LAUNCH(O, CKH_BF16);                          \
+    } while (0)
+        if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+        else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+        else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef LAUNCH
+        return check_launch("scaled_mm_nvfp4");
+    }
     dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
 #define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_kernel<O, B>), grid, dim3(nv::NT), 0, st, p)
 #define BY_BIAS(O)                                         \

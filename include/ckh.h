@@ -186,16 +186,28 @@ int ckh_scaled_mm_fp8(const void* a, const void* b, const float* scale_a, const 
  * K % 32 == 0.
  * Replaces launch_cublas_gemm_blockwise_fp4_kernel (dlpack_bindings.cpp:59-74,
  * ops/cublas_gemm_nvfp4.cu:297-342); semantics follow eager quantization.py:222-246.
+ * workspace: NULL, or ckh_scaled_mm_nvfp4_workspace_bytes(M, N, K) bytes of device memory
+ * (16-byte aligned) in which small tile grids split K (as ckh_scaled_mm_mxfp8); with less
+ * the call does not split.  Calls running at the same time need workspaces of their own.
  * Argument differences from that launcher: the activation comes first (the launcher takes
- * B before A because cuBLASLt is column-major; the product is the same A B^T); there is no
- * workspace (nothing is allocated or needed) and no `accumulate` flag (its only caller,
+ * B before A because cuBLASLt is column-major; the product is the same A B^T); the
+ * workspace is sized by ckh_scaled_mm_nvfp4_workspace_bytes rather than by the caller's
+ * choice, and there is no `accumulate` flag (its only caller,
  * backends/cuda/__init__.py:353, always passes false, i.e. out is overwritten); bias_code
  * names the bias dtype, which that launcher takes from the DLPack tensor.
  */
 int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void* sb,
                         const void* alpha, const void* bias, void* out, int64_t M,
-                        int64_t N, int64_t K, int out_code, int bias_code,
-                        uintptr_t stream);
+                        int64_t N, int64_t K, int out_code, int bias_code, void* workspace,
+                        int64_t workspace_bytes, uintptr_t stream);
+
+/*
+ * Bytes of device workspace ckh_scaled_mm_nvfp4 uses at this shape to split K (0: no
+ * split): grids of at most 128 output tiles of 256 x 256 with K of at least 2048.  No
+ * counterpart in the reference (its launcher takes a cuBLASLt workspace of the caller's
+ * size).
+ */
+int64_t ckh_scaled_mm_nvfp4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*
  * Dynamic per-tensor scale: *scale_out = float(round_x(amax(|x|) * RN32(1/divisor))),

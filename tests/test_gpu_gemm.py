@@ -299,6 +299,56 @@ def test_scaled_mm_nvfp4_skinny_bias_and_alpha(bias_dtype, m, hip):
     assert rel_l2(got, want) <= REL_L2[torch.float32]
 
 
+def _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias=None):
+    """ckh_scaled_mm_nvfp4 through the C ABI with an explicit workspace (None: no split)."""
+    import comfy_kitchen.backends.hip as hb
+
+    m, kb = qx.shape
+    n = qw.shape[0]
+    alpha = (gx * gw).float().reshape(1)
+    out = torch.empty(m, n, dtype=out_dtype, device="cuda")
+    hb._call("ckh_scaled_mm_nvfp4", qx.data_ptr(), qw.data_ptr(), sx.data_ptr(), sw.data_ptr(), alpha.data_ptr(),
+             None if bias is None else bias.data_ptr(), out.data_ptr(), m, n, 2 * kb, hb.DTYPE_TO_CODE[out_dtype],
+             0 if bias is None else hb.DTYPE_TO_CODE[bias.dtype], None if ws is None else ws.data_ptr(),
+             0 if ws is None else ws.numel(), torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(256, 4096, 2048), (300, 2000, 4160), (129, 520, 5152), (65, 13824, 2048)])
+def test_scaled_mm_nvfp4_split_k(m, n, k, out_dtype, hip):
+    """Small NVFP4 tile grids split K into a workspace (ranges of an even number of
+    256-element groups; a last range shorter than the others, K % 256 != 0, rows past M,
+    columns past N), against the oracle and against the unsplit call (fp32 summation order
+    only); the reduce kernel applies alpha and bias."""
+    import comfy_kitchen.backends.hip as hb
+
+    nbytes = hb._lib.ckh_scaled_mm_nvfp4_workspace_bytes(m, n, k)
+    assert nbytes > 0
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=m + 7 * n + k)
+    bias = (torch.randn(n) * 0.1).float()
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, bias=bias, out_dtype=torch.float32)
+    qx, sx, qw, sw, gx, gw, bias = qx.cuda(), sx.cuda(), qw.cuda(), sw.cuda(), gx.cuda(), gw.cuda(), bias.cuda()
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    got = _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias)
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+    assert torch.equal(got, _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias))
+    if out_dtype == torch.float32:
+        assert rel_l2(got, _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, None, bias)) <= 1e-6
+    assert torch.equal(ck.scaled_mm_nvfp4(qx, qw, gx, gw, sx, sw, bias=bias, out_dtype=out_dtype), got)
+
+
+def test_scaled_mm_nvfp4_workspace_bytes(hip):
+    import comfy_kitchen.backends.hip as hb
+
+    f = hb._lib.ckh_scaled_mm_nvfp4_workspace_bytes
+    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 20 groups: ranges of 6
+    assert f(8192, 13824, 5120) == 0  # 1728 tiles
+    assert f(64, 13824, 5120) == 0  # skinny kernel
+    assert f(256, 13824, 1024) == 0  # 4 groups
+    assert f(0, 4096, 8192) == 0
+
+
 def test_scaled_mm_nvfp4_skinny_matches_tile_rows(hip):
     """Rows of a 65-row product (tile kernel) against the same rows computed alone (skinny
     kernel): both sum exact fp16 products in fp32 MFMAs, so they agree to fp32 rounding."""
