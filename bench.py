@@ -339,6 +339,13 @@ LINEAR_SHAPES = [
     ("flux_qkv", 4608, 9216, 3072), ("flux_proj", 4608, 3072, 3072), ("flux_mlp_up", 4608, 12288, 3072),
     ("flux_mlp_down", 4608, 3072, 12288), ("flux_mod_m1", 1, 18432, 3072), ("flux_mod_m16", 16, 18432, 3072),
     ("wan_attn", 8192, 5120, 5120), ("wan_ffn_up", 8192, 13824, 5120), ("wan_ffn_down", 8192, 5120, 13824),
+    # short activations (e.g. a text prompt's tokens): small tile grids, split-K or half tiles
+    ("m256_flux_mod", 256, 18432, 3072), ("m256_wan_ffn_up", 256, 13824, 5120), ("m256_wan_ffn_down", 256, 5120, 13824),
+]
+# NVFP4 linears (no vendor NVFP4 GEMM on this stack): skinny, split-K and full tile grids
+NV_LINEAR_SHAPES = [
+    ("wan_ffn_up_m1", 1, 13824, 5120), ("wan_ffn_up_m16", 16, 13824, 5120), ("wan_ffn_up_m64", 64, 13824, 5120),
+    ("wan_ffn_up_m256", 256, 13824, 5120), ("wan_ffn_down_m256", 256, 5120, 13824), ("flux_mod_m1", 1, 18432, 3072),
 ]
 
 
@@ -440,6 +447,41 @@ def run_linear_shapes(steps: int, warmup: int, log) -> dict:
         log(f"linear {name} [{m}, {n}, {k}]: " + ", ".join(
             f"{key} {e[key]['ms'] * 1e3:.1f} us" for key in ("mx", "fp8", "vendor_fp8", "vendor_mx") if key in e))
         del qa, sa, qw, sw
+    return res
+
+
+def run_nv_linear_shapes(steps: int, warmup: int, log) -> dict:
+    """ops.nv_linear_shapes: ck.scaled_mm_nvfp4 on each NV_LINEAR_SHAPES entry (bf16 operands
+    N(0, 1) and N(0, 0.02) quantized by ck.quantize_nvfp4 with amax/2688 global scales), graph-
+    timed over rotating weight sets: TFLOPS against the dense f16 peak the kernel computes at,
+    and for M <= 256 the weight bytes (codes + scales) per second against HBM peak."""
+    import comfy_kitchen as ck
+
+    dev = torch.device("cuda", 0)
+    res = {}
+    for i, (name, m, n, k) in enumerate(NV_LINEAR_SHAPES):
+        g = torch.Generator(device=dev).manual_seed(200 + i)
+        x = torch.randn(m, k, device=dev, generator=g).bfloat16()
+        w = (torch.randn(n, k, device=dev, generator=g) * 0.02).bfloat16()
+        gx, gw = ck.amax_scale(x, 2688.0), ck.amax_scale(w, 2688.0)
+        qa, sa = ck.quantize_nvfp4(x, gx)
+        qw, sw = ck.quantize_nvfp4(w, gw)
+        ref = ck.scaled_mm_nvfp4(qa, qw, gx, gw, sa, sw)
+        nset = _sets_for(qa.numel() + qw.numel())
+        ws = [(qw.clone(), sw.clone()) for _ in range(nset)]
+        ms = time_graph(lambda i_: (lambda: ck.scaled_mm_nvfp4(qa, ws[i_][0], gx, gw, sa, ws[i_][1])), nset,
+                        max(steps // 2, 10), warmup,
+                        check=lambda outs: [torch.equal(o, ref) or sys.exit("graph mismatch nv linear") for o in outs])
+        flops = 2 * m * n * k
+        wb = qw.numel() + sw.numel()
+        e = {"M": m, "N": n, "K": k, "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+             "frac_f16_peak": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        if m <= 256:
+            gbs = wb / (ms * 1e-3) / 1e9
+            e.update({"weight_gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        res[name] = e
+        log(f"nv linear {name} [{m}, {n}, {k}]: {ms * 1e3:.1f} us")
+        del ws, x, w, qa, sa, qw, sw
     return res
 
 
@@ -1217,10 +1259,17 @@ def main():
     gpu = run_gpu(configs, args.steps, args.warmup, log)
     if "lin" in configs:
         gpu["linear_shapes"] = run_linear_shapes(args.steps, args.warmup, log)
+        gpu["nv_linear_shapes"] = run_nv_linear_shapes(args.steps, args.warmup, log)
     sweep = run_copy_sweep(log) if "sweep" in configs else None
     cpu = {} if args.no_cpu else run_cpu_baseline(configs, log)
 
-    primary = "quantize_mxfp8" if "quantize_mxfp8" in gpu else next(iter(gpu))
+    # the headline op: quantize_mxfp8 (config 3), else the first op measured with a roofline
+    with_roof = [k for k, v in gpu.items() if isinstance(v, dict) and "bound" in v]
+    if not with_roof:
+        print(json.dumps({"metric": METRIC, "ops": gpu, "copy_sweep": sweep, "note": "no roofline op in --configs"}),
+              flush=True)
+        return
+    primary = "quantize_mxfp8" if "quantize_mxfp8" in gpu else with_roof[0]
     p = gpu[primary]
     roof = {k: p[k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
     roof["traffic_counts"] = "L2-miss bytes per launch (TCC FETCH_SIZE + WRITE_SIZE): HBM plus Infinity-Cache hits"
