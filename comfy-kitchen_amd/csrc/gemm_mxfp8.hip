@@ -671,7 +671,38 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
 // (lane l = 32 h + r: row r, bytes k0 + 16 h and k0 + 32 + 16 h; scale word shifted by
 // 8 h, opsel 0 / 2 for even / odd steps of a 128-wide scale block).  Rows past M or N and
 // bytes past K lie outside the buffer descriptors and load as zeros.
-namespace sk {
+namespace mxsk {
+
+using namespace ckh::sk;
+
+constexpr int kSkRow = 256;              // staged bytes per row and chunk
+constexpr int kSkCpr = kSkRow / 16;      // 16-byte chunks per staged row
+constexpr int kSkRpl = 1024 / kSkRow;    // staged rows per direct-to-LDS load (1 KB)
+
+// Staging layout: row r of a chunk is 256 bytes; logical 16-byte chunk c sits at physical
+// chunk c ^ (r % 16).  LDS banks repeat every 256 bytes, so a fragment read (16 lanes = 16
+// consecutive rows, one logical chunk) hits 16 distinct 16-byte bank groups.
+__device__ __forceinline__ uint32_t sk_swz(int r) { return static_cast<uint32_t>(r & (kSkCpr - 1)); }
+
+// Direct-to-LDS whole-line loads of rows [0, NQ * kSkRpl) of a chunk: load q writes 1 KB,
+// rows kSkRpl q .. , lane i to row kSkRpl q + i / kSkCpr, physical chunk i % kSkCpr, so each
+// load reads 8 whole 128-byte lines.  Bytes past K, and rows outside the descriptor, arrive
+// as zeros.
+template <int NQ, int AUX>
+__device__ __forceinline__ void stage_rows256(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int K, int kbase, int lane) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const int row = kSkRpl * q + lane / kSkCpr;
+        const int k = kbase + static_cast<int>(((lane % kSkCpr) ^ sk_swz(row)) << 4);
+        const uint32_t off = k < K ? static_cast<uint32_t>(row * K + k) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + q * 1024), 16, off, 0, 0, AUX);
+    }
+}
+
+// Logical 16-byte chunk c of staged row r.
+__device__ __forceinline__ v4u staged_chunk256(const uint8_t* st, int r, int c) {
+    return *reinterpret_cast<const v4u*>(st + r * kSkRow + ((static_cast<uint32_t>(c) ^ sk_swz(r)) << 4));
+}
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -695,8 +726,8 @@ struct Args {
 // This lane's MFMA operand for step j of the staged chunk: row r, logical chunks 4 j + h and
 // 4 j + 2 + h (bytes k0 + 16 h and k0 + 32 + 16 h of the step).
 __device__ __forceinline__ v8i staged_frag(const uint8_t* st, int r, int h, int j) {
-    const v4u x = staged_chunk(st, r, 4 * j + h);
-    const v4u y = staged_chunk(st, r, 4 * j + 2 + h);
+    const v4u x = staged_chunk256(st, r, 4 * j + h);
+    const v4u y = staged_chunk256(st, r, 4 * j + 2 + h);
     return v8i{(int)x[0], (int)x[1], (int)x[2], (int)x[3], (int)y[0], (int)y[1], (int)y[2], (int)y[3]};
 }
 
@@ -763,8 +794,8 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
         const int s0 = c * kSkChunk;
         // the weight is read once (nontemporal); the activation, which every workgroup
         // reads, stays cached
-        stage_rows<WR / kSkRpl, kAuxNontemporal>(rb, stb, p.K, s0 * 64, lane);
-        if constexpr (AR > 0) stage_rows<AR / kSkRpl, 0>(ra[0], stb + WR * kSkRow, p.K, s0 * 64, lane);
+        stage_rows256<WR / kSkRpl, kAuxNontemporal>(rb, stb, p.K, s0 * 64, lane);
+        if constexpr (AR > 0) stage_rows256<AR / kSkRpl, 0>(ra[0], stb + WR * kSkRow, p.K, s0 * 64, lane);
         if constexpr (!UNIT) {
 #pragma unroll
             for (int u = 0; u < kSkChunk / 2; ++u) {
@@ -802,7 +833,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     if (wave < NC) issue(wave, cur);
     for (int c = wave; c < NC; c += WV) {
         __asm__ volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(mx::waitcnt_vm_lgkm0(0));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
         __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int j = 0; j < kSkChunk; ++j) {
@@ -833,7 +864,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
         }
         // the next chunk's loads overwrite the staged rows: every fragment read is done
         __asm__ volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(mx::waitcnt_vm_lgkm0(63));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
         __asm__ volatile("" ::: "memory");
         if (c + WV < NC) issue(c + WV, cur);
     }
@@ -885,7 +916,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     }
 }
 
-}  // namespace sk
+}  // namespace mxsk
 }  // namespace ckh
 
 using namespace ckh;
@@ -912,20 +943,22 @@ void launch_grid(const mx::Args& p, unsigned wgs, int out_code, int bias_code, b
 #undef LAUNCH
 }
 
-// Activations of at most kSkinnyMaxM rows take the skinny kernel (sk::gemm_skinny_kernel).
+// Activations of at most kSkinnyMaxM rows take the skinny kernel (mxsk::gemm_skinny_kernel).
 constexpr int kSkinnyMaxM = 64;
 
 template <bool UNIT>
 int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-    sk::Args p{};
+    mxsk::Args p{};
     p.a = q.a; p.b = q.b; p.sa = q.sa; p.sb = q.sb; p.bias = q.bias; p.out = q.out;
     p.M = q.M; p.N = q.N; p.K = q.K; p.ncb = q.ncb; p.sa_rows = q.sa_rows; p.sb_rows = q.sb_rows;
     p.tsa = q.tsa; p.tsb = q.tsb;
     // per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
     // staged activation rows (measured on N = 18432, K = 3072: M = 1 12.7 us, M = 16 15.4 us,
-    // M = 32 20.5 us, M = 64 26.4 us)
+    // M = 32 20.5 us, M = 64 26.4 us).  The NVFP4 skinny kernel's form (128-byte chunks, two
+    // in flight per wave) measured slower here, where a chunk costs only a few MFMAs: M = 1
+    // 14.5 against 12.9 us, M = 16 15.9 against 15.5, M = 64 29.6 against 26.5 (same process).
 #define LAUNCH(O, B, WV, NT, MT, AR)                                                              \
-    hipLaunchKernelGGL((sk::gemm_skinny_kernel<O, B, UNIT, WV, NT, MT, AR>),                      \
+    hipLaunchKernelGGL((mxsk::gemm_skinny_kernel<O, B, UNIT, WV, NT, MT, AR>),                    \
                        dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
 #define BY_MT(O, B)                                    \
     do {                                               \

@@ -529,17 +529,13 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
 // zeros.
 namespace nvsk {
 
+using namespace ckh::sk;
 using ckh::v8h;
 using ckh::v2h;
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef unsigned v2u __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kCb = 128;             // code bytes per row and chunk
 constexpr int kStages = kCb / 32;    // 64-element stages (and scale words of a row) per chunk: 4
 constexpr int kApitch = 2 * 2 * kCb + 16;  // bytes of one decoded fp16 activation row (+16 pad)
-constexpr int kAuxNontemporal = 2;   // buffer-load cache policy bit: the weight is read once
 
 struct Args {
     const uint8_t* a;
@@ -553,24 +549,6 @@ struct Args {
     int ncb;               // scale word columns: ceil(K/16/4)
     int sa_rows, sb_rows;  // padded scale rows (multiples of 128)
 };
-
-// Staged weight rows are 128 bytes; logical 16-byte chunk c of row r sits at physical chunk
-// c ^ (r % 8) ^ ((r / 8) % 2), so the 16 rows of a fragment read (one logical chunk each)
-// hit 16 distinct 16-byte groups of the 256-byte bank cycle.
-__device__ __forceinline__ uint32_t swz8(int r) { return static_cast<uint32_t>((r & 7) ^ ((r >> 3) & 1)); }
-
-// Direct-to-LDS loads of a chunk of 32 NT weight rows: load q writes 1 KB (rows 8 q .. 8 q + 7),
-// lane i to row 8 q + i / 8, physical chunk i % 8, i.e. 8 whole 128-byte lines per load.
-template <int NQ>
-__device__ __forceinline__ void stage_weight(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int Kb, int b0, int lane) {
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-        const int row = 8 * q + (lane >> 3);
-        const int k = b0 + static_cast<int>(((lane & 7) ^ swz8(row)) << 4);
-        const uint32_t off = k < Kb ? static_cast<uint32_t>(row * Kb + k) : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + q * 1024), 16, off, 0, 0, kAuxNontemporal);
-    }
-}
 
 // One chunk's register-held operands.
 template <int NT, int MT, int AR>
@@ -613,26 +591,7 @@ constexpr int loads_per_chunk() {
     return 4 * NT + kStages + (AR > 0 ? 2 * (AR / 8) : MT * kStages + kStages);
 }
 
-// n consecutive scale words (n = 1 or 2) from offset off of a swizzled scale tensor
-template <int N>
-__device__ __forceinline__ void load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[N]) {
-    if constexpr (N == 2) {
-        const v2u x = __builtin_bit_cast(v2u, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
-        w[0] = x[0];
-        w[1] = x[1];
-    } else {
-        w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-    }
-}
-
 __device__ __forceinline__ v2h bcast(_Float16 x) { return v2h{x, x}; }
-
-template <int WAITCNT>
-__device__ __forceinline__ void wait() {
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(WAITCNT);
-    __asm__ volatile("" ::: "memory");
-}
 
 // WV: waves per workgroup, each taking every WV-th K chunk.
 // NT: 32-row weight tiles per workgroup (1 or 2).
@@ -657,7 +616,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5, r = lane & 31;
-    const int n0 = sk::xcd_group(blockIdx.x, gridDim.x) * WR;
+    const int n0 = xcd_group(blockIdx.x, gridDim.x) * WR;
     const int Kb = p.K / 2;  // code bytes per row
 
     const __amdgpu_buffer_rsrc_t rb =
@@ -673,7 +632,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     // offset ((row/128 * ncb + c) * 32 + row%32) * 16 + ((row%128)/32) * 4; the second tile's
     // word follows it (n0 is a multiple of 64 when NT = 2).  Activation row i (< 128):
     // (i%32) * 16 + (i/32) * 4.
-    const uint32_t sb_row = static_cast<uint32_t>((n0 >> 7) * p.ncb * 512 + r * 16 + ((n0 & 127) >> 5) * 4);
+    const uint32_t sb_row = weight_word_offset(n0, r, p.ncb);
     const int NC = (Kb + kCb - 1) / kCb;
 
     uint8_t* wbuf = lds + wave * WST;           // this wave's D weight buffers
@@ -687,7 +646,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     // (the lambdas are forced inline: an outlined step would keep R in scratch memory)
     auto issue = [&](int c, uint8_t* buf, Regs<NT, MT, AR>& R) __attribute__((always_inline)) {
         const int b0 = c * kCb;  // first code byte of the chunk
-        stage_weight<4 * NT>(rb, buf, Kb, b0, lane);
+        stage_rows<4 * NT, kAuxNontemporal>(rb, buf, Kb, b0, lane);
 #pragma unroll
         for (int j = 0; j < kStages; ++j) {
             const int col = c * kStages + j;
@@ -800,11 +759,11 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     }, std::make_integer_sequence<int, D>{});
     auto step = [&](int i, auto d_c) __attribute__((always_inline)) {
         constexpr int d = decltype(d_c)::value;
-        wait<nv::waitcnt_vm_lgkm0((D - 1) * LPC)>();  // chunk i's loads are done
+        wait<waitcnt_vm_lgkm0((D - 1) * LPC)>();  // chunk i's loads are done
         pin(R[d]);
         compute(wbuf + d * WB, R[d]);
         // the loads of chunk i + D overwrite this buffer: every read of it is done
-        wait<nv::waitcnt_vm_lgkm0(63)>();
+        wait<waitcnt_vm_lgkm0(63)>();
         issue(wave + (i + D) * WV, wbuf + d * WB, R[d]);
     };
     int i = 0;
@@ -814,7 +773,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     nv::for_each_index([&](auto d_c) {
         if (i + decltype(d_c)::value < n) step(i + decltype(d_c)::value, d_c);
     }, std::make_integer_sequence<int, D - 1>{});
-    wait<nv::waitcnt_vm_lgkm0(0)>();  // the trailing loads write LDS, which is reused below
+    wait<waitcnt_vm_lgkm0(0)>();  // the trailing loads write LDS, which is reused below
 
     // the K partials of each 32 x 32 tile meet in LDS (reusing the staging area); wave w adds
     // and stores registers RPW w .. RPW w + RPW - 1 (columns n0 + 32 u + 8 (v / 4) + 4 h + v % 4
