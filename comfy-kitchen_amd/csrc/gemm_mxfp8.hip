@@ -883,35 +883,41 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
             for (int v = 0; v < 16; ++v) red[wave][u][t][v][lane] = acc[u][t][v];
     __syncthreads();
     const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
+    // registers v .. v + G - 1 of a group hold consecutive columns (G <= 4, v % G == 0)
+    constexpr int G = RPW < 4 ? RPW : 4;
     const int v0 = RPW * wave;
 #pragma unroll
     for (int u = 0; u < NT; ++u) {
-        const int n = n0 + 32 * u + 8 * (v0 >> 2) + 4 * h + (v0 & 3);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             const int m = 32 * t + r;
-            float v[RPW];
 #pragma unroll
-            for (int e = 0; e < RPW; ++e) {
-                float s = 0.0f;
+            for (int g0 = 0; g0 < RPW; g0 += G) {
+                const int vb = v0 + g0;
+                const int n = n0 + 32 * u + 8 * (vb >> 2) + 4 * h + (vb & 3);
+                float v[G];
 #pragma unroll
-                for (int w = 0; w < WV; ++w) s += red[w][u][t][v0 + e][lane];
-                if constexpr (UNIT) s *= alpha;
-                if constexpr (BIAS >= 0) s += n + e < p.N ? load1<BIAS>(p.bias, n + e) : 0.0f;
-                // kept from being fused with the narrowing into one mixed-precision rounding
-                v[e] = (UNIT || BIAS >= 0) ? opaque(s) : s;
-            }
-            if (m >= p.M) continue;
-            const int64_t idx = static_cast<int64_t>(m) * p.N + n;
-            if constexpr (RPW == 4) {
-                if (n + 3 < p.N && (p.N & 3) == 0) {
-                    mx::store4<OUT>(p.out, idx, v);
-                    continue;
+                for (int e = 0; e < G; ++e) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < WV; ++w) s += red[w][u][t][vb + e][lane];
+                    if constexpr (UNIT) s *= alpha;
+                    if constexpr (BIAS >= 0) s += n + e < p.N ? load1<BIAS>(p.bias, n + e) : 0.0f;
+                    // kept from being fused with the narrowing into one mixed-precision rounding
+                    v[e] = (UNIT || BIAS >= 0) ? opaque(s) : s;
                 }
-            }
+                if (m >= p.M) continue;
+                const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+                if constexpr (G == 4) {
+                    if (n + 3 < p.N && (p.N & 3) == 0) {
+                        mx::store4<OUT>(p.out, idx, v);
+                        continue;
+                    }
+                }
 #pragma unroll
-            for (int e = 0; e < RPW; ++e)
-                if (n + e < p.N) mx::store1<OUT>(p.out, idx + e, v[e]);
+                for (int e = 0; e < G; ++e)
+                    if (n + e < p.N) mx::store1<OUT>(p.out, idx + e, v[e]);
+            }
         }
     }
 }
@@ -954,7 +960,10 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
     p.tsa = q.tsa; p.tsb = q.tsb;
     // per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
     // staged activation rows (measured on N = 18432, K = 3072: M = 1 12.7 us, M = 16 15.4 us,
-    // M = 32 20.5 us, M = 64 26.4 us).  The NVFP4 skinny kernel's form (128-byte chunks, two
+    // M = 32 20.5 us, M = 64 26.4 us).  With 16 activation rows the waves per workgroup
+    // follow N: 2 waves when there are at least 256 workgroups (M = 16, N = 18432: 14.6
+    // against 15.4 us with 4), 8 when there are fewer than 128 (N = 3072, K = 12288: 16.6
+    // against 17.2 us; with 2 waves 25.9 us).  The NVFP4 skinny kernel's form (128-byte chunks, two
     // in flight per wave) measured slower here, where a chunk costs only a few MFMAs: M = 1
     // 14.5 against 12.9 us, M = 16 15.9 against 15.5, M = 64 29.6 against 26.5 (same process).
 #define LAUNCH(O, B, WV, NT, MT, AR)                                                              \
@@ -962,10 +971,12 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
                        dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
 #define BY_MT(O, B)                                    \
     do {                                               \
-        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);        \
-        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16); \
-        else if (p.M <= 32) LAUNCH(O, B, 4, 2, 1, 0);  \
-        else LAUNCH(O, B, 4, 2, 2, 0);                 \
+        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);                       \
+        else if (p.M <= 16 && p.N >= 8192) LAUNCH(O, B, 2, 1, 1, 16); \
+        else if (p.M <= 16 && p.N >= 4096) LAUNCH(O, B, 4, 1, 1, 16); \
+        else if (p.M <= 16) LAUNCH(O, B, 8, 1, 1, 16);                \
+        else if (p.M <= 32) LAUNCH(O, B, 4, 2, 1, 0);                 \
+        else LAUNCH(O, B, 4, 2, 2, 0);                                \
     } while (0)
 #define BY_BIAS(O)                                          \
     do {                                                    \

@@ -789,32 +789,38 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
             for (int v = 0; v < 16; ++v) red[wave][u][t][v][lane] = acc[u][t][v];
     __syncthreads();
     const float alpha = p.alpha[0];
+    // registers v .. v + G - 1 of a group hold consecutive columns (G <= 4, v % G == 0)
+    constexpr int G = RPW < 4 ? RPW : 4;
     const int v0 = RPW * wave;
 #pragma unroll
     for (int u = 0; u < NT; ++u) {
-        const int n = n0 + 32 * u + 8 * (v0 >> 2) + 4 * h + (v0 & 3);
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
             const int m = 32 * t + r;
-            float v[RPW];
 #pragma unroll
-            for (int e = 0; e < RPW; ++e) {
-                float s = 0.0f;
+            for (int g0 = 0; g0 < RPW; g0 += G) {
+                const int vb = v0 + g0;
+                const int n = n0 + 32 * u + 8 * (vb >> 2) + 4 * h + (vb & 3);
+                float v[G];
 #pragma unroll
-                for (int w = 0; w < WV; ++w) s += red[w][u][t][v0 + e][lane];
-                v[e] = s * alpha + (n + e < p.N ? nv::bias_at<BIAS>(p.bias, n + e) : 0.0f);
-            }
-            if (m >= p.M) continue;
-            const int64_t idx = static_cast<int64_t>(m) * p.N + n;
-            if constexpr (RPW == 4) {
-                if (n + 3 < p.N && (p.N & 3) == 0) {
-                    nv::store4<OUT>(p.out, idx, v);
-                    continue;
+                for (int e = 0; e < G; ++e) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < WV; ++w) s += red[w][u][t][vb + e][lane];
+                    v[e] = s * alpha + (n + e < p.N ? nv::bias_at<BIAS>(p.bias, n + e) : 0.0f);
                 }
-            }
+                if (m >= p.M) continue;
+                const int64_t idx = static_cast<int64_t>(m) * p.N + n;
+                if constexpr (G == 4) {
+                    if (n + 3 < p.N && (p.N & 3) == 0) {
+                        nv::store4<OUT>(p.out, idx, v);
+                        continue;
+                    }
+                }
 #pragma unroll
-            for (int e = 0; e < RPW; ++e)
-                if (n + e < p.N) nv::store1<OUT>(p.out, idx + e, v[e]);
+                for (int e = 0; e < G; ++e)
+                    if (n + e < p.N) nv::store1<OUT>(p.out, idx + e, v[e]);
+            }
         }
     }
 }
