@@ -38,10 +38,23 @@ def _input(seed, rows=64, cols=256):
     return torch.randn(rows, cols, device="cuda", generator=g).bfloat16()
 
 
+# (rows, in_features, hidden, out_features): 64 rows run the skinny GEMM kernels; 256 rows
+# against K = 4096 and 512 outputs split K over a workspace (two launches per GEMM)
+SHAPES = [(64, 256, 512, 128), (256, 4096, 512, 128)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=["skinny", "split_k"])
 @pytest.mark.parametrize("layout", LAYOUTS)
-def test_graph_capture_replay(layout, hip):
-    model = TwoLayer(layout)
-    x = _input(1)
+def test_graph_capture_replay(layout, shape, hip):
+    rows, fin, hidden, fout = shape
+    model = TwoLayer(layout, in_features=fin, hidden=hidden, out_features=fout)
+    if shape[0] == 256:
+        import comfy_kitchen.backends.hip as hb
+
+        fn = ("ckh_scaled_mm_nvfp4_workspace_bytes" if layout == "TensorCoreNVFP4Layout"
+              else "ckh_scaled_mm_workspace_bytes")
+        assert getattr(hb._lib, fn)(rows, hidden, fin) > 0  # the first GEMM splits K
+    x = _input(1, rows, fin)
     with torch.no_grad():
         want = model(x)
         static_x = x.clone()
@@ -59,11 +72,11 @@ def test_graph_capture_replay(layout, hip):
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(static_out, want), f"replay {i} differs from eager"
-            eager = model(_input(10 + i))
+            eager = model(_input(10 + i, rows, fin))
             torch.cuda.synchronize()
             assert eager.shape == want.shape
         # a new input through the same graph
-        x2 = _input(2)
+        x2 = _input(2, rows, fin)
         static_x.copy_(x2)
         graph.replay()
         torch.cuda.synchronize()
