@@ -752,7 +752,8 @@ struct SkRegs {
 // the activation's fragments are loaded straight into registers.
 template <int OUT, int BIAS, bool UNIT, int WV, int NT, int MT, int AR>
 __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
-    static_assert(AR == 0 || (MT == 1 && AR % kSkRpl == 0 && AR <= 32), "staged activation: one tile");
+    static_assert(AR == 0 || (AR % kSkRpl == 0 && AR <= 32 * MT && AR > 32 * (MT - 1)),
+                  "staged activation rows: within the MT tiles, a multiple of the rows per load");
     static_assert(16 % WV == 0, "each wave stores 16 / WV accumulator registers");
     constexpr int WR = 32 * NT;                   // weight rows of the workgroup
     constexpr int WST = (WR + AR) * kSkRow;       // staged bytes per wave
@@ -771,6 +772,8 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     for (int t = 0; t < MT; ++t)
         ra[t] = buffer_rsrc(p.a + static_cast<int64_t>(32 * t) * p.K,
                             static_cast<uint32_t>(max(0, min(32, p.M - 32 * t))) * p.K);
+    // the staged activation rows (AR > 0): rows past M read as zeros
+    const __amdgpu_buffer_rsrc_t ras = buffer_rsrc(p.a, static_cast<uint32_t>(max(0, min(AR, p.M))) * p.K);
     // per-tensor mode: no scale tensors (zero-sized descriptors, never loaded)
     const __amdgpu_buffer_rsrc_t rsb = buffer_rsrc(p.sb, UNIT ? 0u : static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rsa = buffer_rsrc(p.sa, UNIT ? 0u : static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
@@ -795,7 +798,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
         // the weight is read once (nontemporal); the activation, which every workgroup
         // reads, stays cached
         stage_rows256<WR / kSkRpl, kAuxNontemporal>(rb, stb, p.K, s0 * 64, lane);
-        if constexpr (AR > 0) stage_rows256<AR / kSkRpl, 0>(ra[0], stb + WR * kSkRow, p.K, s0 * 64, lane);
+        if constexpr (AR > 0) stage_rows256<AR / kSkRpl, 0>(ras, stb + WR * kSkRow, p.K, s0 * 64, lane);
         if constexpr (!UNIT) {
 #pragma unroll
             for (int u = 0; u < kSkChunk / 2; ++u) {
@@ -841,8 +844,9 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 if constexpr (AR > 0) {
-                    fa[t] = staged_frag(stb + WR * kSkRow, r < AR ? r : 0, h, j);
-                    if (r >= AR) fa[t] = v8i{};
+                    const int row = 32 * t + r;
+                    fa[t] = staged_frag(stb + WR * kSkRow, row < AR ? row : 0, h, j);
+                    if (row >= AR) fa[t] = v8i{};
                 } else {
                     const v4u u = cur.al[t][j][0], w = cur.al[t][j][1];
                     fa[t] = v8i{(int)u[0], (int)u[1], (int)u[2], (int)u[3], (int)w[0], (int)w[1], (int)w[2], (int)w[3]};
@@ -960,10 +964,19 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
     p.tsa = q.tsa; p.tsb = q.tsb;
     // per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
     // staged activation rows (measured on N = 18432, K = 3072: M = 1 12.7 us, M = 16 15.4 us,
-    // M = 32 20.5 us, M = 64 26.4 us).  With 16 activation rows the waves per workgroup
+    // M = 32 20.5 us, M = 64 26.4 us, the last two with the activation fragments loaded
+    // straight into registers).  With 16 activation rows the waves per workgroup
     // follow N: 2 waves when there are at least 256 workgroups (M = 16, N = 18432: 14.6
     // against 15.4 us with 4), 8 when there are fewer than 128 (N = 3072, K = 12288: 16.6
-    // against 17.2 us; with 2 waves 25.9 us).  The NVFP4 skinny kernel's form (128-byte chunks, two
+    // against 17.2 us; with 2 waves 25.9 us).  From 17 rows on, staging the activation
+    // through LDS too (32 or 64 rows) pays where the workgroups stay small enough in LDS to
+    // share CUs (same process, against the register-loaded fragments): M = 32, N = 18432
+    // 17.3 against 20.5 us (4 waves, one weight tile); N = 5120, K = 5120 10.8 against 16.5
+    // (8 waves); M = 64, N = 18432 21.7 against 26.3 (2 waves, two tiles); N = 5120,
+    // K = 13824 29.3 against 47.4 and N = 3072, K = 12288 25.4 against 42.1 (4 waves, one
+    // tile); for N from 8192 to 16383 two weight tiles with 32 staged rows (M = 24,
+    // N = 13824 17.2 against 17.8) or register-loaded fragments (M = 48: 21.0, staged 64 rows
+    // 21.0 with 4 waves, 24.4 with 2).  The NVFP4 skinny kernel's form (128-byte chunks, two
     // in flight per wave) measured slower here, where a chunk costs only a few MFMAs: M = 1
     // 14.5 against 12.9 us, M = 16 15.9 against 15.5, M = 64 29.6 against 26.5 (same process).
 #define LAUNCH(O, B, WV, NT, MT, AR)                                                              \
@@ -971,12 +984,16 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
                        dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
 #define BY_MT(O, B)                                    \
     do {                                               \
-        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);                       \
-        else if (p.M <= 16 && p.N >= 8192) LAUNCH(O, B, 2, 1, 1, 16); \
-        else if (p.M <= 16 && p.N >= 4096) LAUNCH(O, B, 4, 1, 1, 16); \
-        else if (p.M <= 16) LAUNCH(O, B, 8, 1, 1, 16);                \
-        else if (p.M <= 32) LAUNCH(O, B, 4, 2, 1, 0);                 \
-        else LAUNCH(O, B, 4, 2, 2, 0);                                \
+        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);                        \
+        else if (p.M <= 16 && p.N >= 8192) LAUNCH(O, B, 2, 1, 1, 16);  \
+        else if (p.M <= 16 && p.N >= 4096) LAUNCH(O, B, 4, 1, 1, 16);  \
+        else if (p.M <= 16) LAUNCH(O, B, 8, 1, 1, 16);                 \
+        else if (p.M <= 32 && p.N >= 16384) LAUNCH(O, B, 4, 1, 1, 32); \
+        else if (p.M <= 32 && p.N >= 8192) LAUNCH(O, B, 4, 2, 1, 32);  \
+        else if (p.M <= 32) LAUNCH(O, B, 8, 1, 1, 32);                 \
+        else if (p.N >= 16384) LAUNCH(O, B, 2, 2, 2, 64);              \
+        else if (p.N >= 8192) LAUNCH(O, B, 4, 2, 2, 0);                \
+        else LAUNCH(O, B, 4, 1, 2, 64);                                \
     } while (0)
 #define BY_BIAS(O)                                          \
     do {                                                    \

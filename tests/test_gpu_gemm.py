@@ -111,12 +111,15 @@ def test_scaled_mm_mxfp8_config4_full(hip):
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 3072), (8, 200, 288), (9, 64, 1024), (16, 1000, 3072), (17, 1000, 3072),
                                    (31, 96, 224), (32, 4096, 64), (33, 130, 5120), (40, 33, 96), (64, 512, 1056),
-                                   (2, 33, 32), (48, 18432, 128), (12, 8200, 320), (16, 4096, 3072)])
+                                   (2, 33, 32), (48, 18432, 128), (12, 8200, 320), (16, 4096, 3072),
+                                   (20, 16400, 256), (30, 9000, 1088), (64, 16448, 320), (50, 12000, 4096),
+                                   (63, 3000, 12288), (25, 160, 96)])
 def test_scaled_mm_mxfp8_skinny(m, n, k, out_dtype, hip):
     """At most 64 activation rows take the skinny kernel (a workgroup per 32 or 64 weight
-    rows, K split over its waves; configurations by M, boundaries 8 / 16 / 32 / 64, and for
-    9..16 rows 2 / 4 / 8 waves by N): rows past M, columns past N, K % 64 == 32, K past one
-    chunk round and long K."""
+    rows, K split over its waves; configurations by M, boundaries 8 / 16 / 32 / 64, and from
+    9 rows on by N, boundaries 4096 / 8192 / 16384: waves per workgroup, weight tiles, and
+    32 or 64 activation rows staged in LDS or loaded as fragments): rows past M, columns
+    past N, K % 64 == 32, K past one chunk round and long K."""
     qx, sx, qw, sw = mx_operands(m, n, k, seed=m * 13 + n + k)
     want = ref.scaled_mm_mxfp8_ref(qx, qw, sx, sw, out_dtype=torch.float32)
     got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
