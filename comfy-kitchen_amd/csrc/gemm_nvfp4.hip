@@ -551,23 +551,24 @@ struct Args {
 };
 
 // One chunk's register-held operands.
-template <int NT, int MT, int AR>
+template <int NT, int MT, int AR, int AS>
 struct Regs {
     uint32_t swb[kStages][NT];  // weight scale words, one per stage
     // AR > 0: the lane's 32 activation elements (row 8 s + lane / 8, 16-byte chunk lane % 8)
     // of each group s of 8 rows, and their scale words
     v4u ac[AR > 0 ? AR / 8 : 1];
     uint32_t aw[AR > 0 ? AR / 8 : 1];
-    // AR == 0: 16 activation code bytes per stage and tile, and the tiles' scale words
-    v4u al[AR > 0 ? 1 : MT][kStages];
+    // AR == 0: the tiles' scale words and, unless the activation codes are staged in LDS
+    // (AS > 0), 16 activation code bytes per stage and tile
+    v4u al[AR > 0 || AS > 0 ? 1 : MT][kStages];
     uint32_t swa[kStages][AR > 0 ? 1 : MT];
 };
 
 // Pin a chunk's registers at this point: the empty asm "modifies" them, so nothing computed
 // from them (e.g. a scale pair) can be hoisted into an earlier step, where it would make the
 // compiler wait for that chunk's loads.
-template <int NT, int MT, int AR>
-__device__ __forceinline__ void pin(Regs<NT, MT, AR>& R) {
+template <int NT, int MT, int AR, int AS>
+__device__ __forceinline__ void pin(Regs<NT, MT, AR, AS>& R) {
 #pragma unroll
     for (int j = 0; j < kStages; ++j) {
 #pragma unroll
@@ -580,15 +581,24 @@ __device__ __forceinline__ void pin(Regs<NT, MT, AR>& R) {
 #pragma unroll
         for (int j = 0; j < kStages; ++j) {
 #pragma unroll
-            for (int t = 0; t < MT; ++t) __asm__ volatile("" : "+v"(R.al[t][j]), "+v"(R.swa[j][t]));
+            for (int t = 0; t < MT; ++t) {
+                __asm__ volatile("" : "+v"(R.swa[j][t]));
+                if constexpr (AS == 0) __asm__ volatile("" : "+v"(R.al[t][j]));
+            }
         }
     }
 }
 
-// vector-memory instructions issue() makes per chunk (for the vmcnt waits)
-template <int NT, int MT, int AR>
-constexpr int loads_per_chunk() {
-    return 4 * NT + kStages + (AR > 0 ? 2 * (AR / 8) : MT * kStages + kStages);
+// Vector-memory instructions issue() makes per chunk (for the vmcnt waits): direct-to-LDS
+// loads (weight rows, staged activation rows) and loads into registers (scale words,
+// activation codes).
+template <int NT, int AS>
+constexpr int lds_loads_per_chunk() {
+    return 4 * NT + AS / 8;
+}
+template <int MT, int AR, int AS>
+constexpr int reg_loads_per_chunk() {
+    return kStages + (AR > 0 ? 2 * (AR / 8) : kStages + (AS > 0 ? 0 : MT * kStages));
 }
 
 __device__ __forceinline__ v2h bcast(_Float16 x) { return v2h{x, x}; }
@@ -599,19 +609,24 @@ __device__ __forceinline__ v2h bcast(_Float16 x) { return v2h{x, x}; }
 // AR: activation rows decoded once per chunk into LDS (8 or 16, >= M, MT = 1), or 0: the
 // activation fragments are decoded in registers.
 // D: chunks in flight per wave (LDS weight buffers).
-template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D>
+// AS (AR = 0): activation rows (32 MT) whose codes are staged in LDS with the weight rows by
+// whole-line loads, or 0: each lane loads its own 16-byte code pieces.
+template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D, int AS = 0>
 __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     static_assert(AR == 0 || (MT == 1 && AR % 8 == 0 && AR <= 16), "decoded activation: 8 or 16 rows");
+    static_assert(AS == 0 || (AR == 0 && AS == 32 * MT), "staged activation codes: whole tiles");
     static_assert(16 % WV == 0, "each wave stores 16 / WV accumulator registers");
     static_assert(NT <= 2 && MT <= 2, "scale words of at most two tiles per load");
     constexpr int WR = 32 * NT;                                   // weight rows of the workgroup
-    constexpr int WB = WR * kCb;                                  // one staged weight chunk
+    constexpr int WB = (WR + AS) * kCb;                           // one staged chunk (weight, activation)
     constexpr int WST = D * WB + (AR > 0 ? AR * kApitch : 0);     // LDS per wave
     constexpr int ZERO = AR > 0 ? kApitch : 0;                    // the zero activation row
     constexpr int RED = WV * NT * MT * 16 * 64 * 4;
     constexpr int LDS = WV * WST + ZERO > RED ? WV * WST + ZERO : RED;
-    constexpr int LPC = loads_per_chunk<NT, MT, AR>();
-    static_assert((D - 1) * LPC < 64, "vmcnt range");
+    // a step's wait: chunk i's register loads and the later chunks' direct-to-LDS loads
+    // may stay in flight (see the step below)
+    constexpr int VM = reg_loads_per_chunk<MT, AR, AS>() + (D - 1) * lds_loads_per_chunk<NT, AS>();
+    static_assert(VM < 64, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -626,6 +641,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     for (int t = 0; t < MT; ++t)
         ra[t] = buffer_rsrc(p.a + static_cast<int64_t>(32 * t) * Kb,
                             static_cast<uint32_t>(max(0, min(32, p.M - 32 * t))) * Kb);
+    const __amdgpu_buffer_rsrc_t ras = buffer_rsrc(p.a, static_cast<uint32_t>(max(0, min(AS, p.M))) * Kb);
     const __amdgpu_buffer_rsrc_t rsb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rsa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     // Scale word of row r of the workgroup's first weight tile in word column c: swizzled
@@ -644,9 +660,12 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     }
 
     // (the lambdas are forced inline: an outlined step would keep R in scratch memory)
-    auto issue = [&](int c, uint8_t* buf, Regs<NT, MT, AR>& R) __attribute__((always_inline)) {
+    auto issue = [&](int c, uint8_t* buf, Regs<NT, MT, AR, AS>& R) __attribute__((always_inline)) {
         const int b0 = c * kCb;  // first code byte of the chunk
+        // the direct-to-LDS loads first; the empty asm keeps the register loads after them
         stage_rows<4 * NT, kAuxNontemporal>(rb, buf, Kb, b0, lane);
+        if constexpr (AS > 0) stage_rows<AS / 8, 0>(ras, buf + WR * kCb, Kb, b0, lane);
+        __asm__ volatile("" ::: "memory");
 #pragma unroll
         for (int j = 0; j < kStages; ++j) {
             const int col = c * kStages + j;
@@ -673,15 +692,17 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
                 const uint32_t co = col < p.ncb ? static_cast<uint32_t>(col * 512) : 0x80000000u;
                 load_words<MT>(rsa, r * 16 + co, R.swa[j]);
             }
+            if constexpr (AS == 0) {
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
+                for (int t = 0; t < MT; ++t)
 #pragma unroll
-                for (int j = 0; j < kStages; ++j) {
-                    const int k = b0 + 32 * j + 16 * h;
-                    R.al[t][j] = __builtin_bit_cast(
-                        v4u, __builtin_amdgcn_raw_buffer_load_b128(
-                                 ra[t], k < Kb ? static_cast<uint32_t>(r * Kb + k) : 0x80000000u, 0, 0));
-                }
+                    for (int j = 0; j < kStages; ++j) {
+                        const int k = b0 + 32 * j + 16 * h;
+                        R.al[t][j] = __builtin_bit_cast(
+                            v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                     ra[t], k < Kb ? static_cast<uint32_t>(r * Kb + k) : 0x80000000u, 0, 0));
+                    }
+            }
         }
     };
 
@@ -697,7 +718,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     const uint32_t wsw = swz8(r);
     const uint8_t* abase = (AR > 0 && r < AR ? actf + r * kApitch : zrow) + 64 * h;
 
-    auto compute = [&](const uint8_t* buf, const Regs<NT, MT, AR>& R) __attribute__((always_inline)) {
+    auto compute = [&](const uint8_t* buf, const Regs<NT, MT, AR, AS>& R) __attribute__((always_inline)) {
         if constexpr (AR > 0) {
             // decode the chunk's activation rows: lane's 32 elements are blocks 2 q, 2 q + 1 of
             // the chunk (bytes 2 (q % 2), +1 of word q / 2)
@@ -722,9 +743,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
                 pb[u] = scale_pair(R.swb[j][u], 16 * h);
             }
             v2h pa[MT];
+            v4u ca[MT];
             if constexpr (AR == 0) {
 #pragma unroll
-                for (int t = 0; t < MT; ++t) pa[t] = scale_pair(R.swa[j][t], 16 * h);
+                for (int t = 0; t < MT; ++t) {
+                    pa[t] = scale_pair(R.swa[j][t], 16 * h);
+                    ca[t] = AS > 0 ? staged_chunk(buf + WR * kCb, 32 * t + r, 2 * j + h) : R.al[t][j];
+                }
             }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
@@ -732,7 +757,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     if constexpr (AR > 0) da[t] = *reinterpret_cast<const v8h*>(abase + 128 * j + 16 * kk);
-                    else da[t] = decode8(R.al[t][j][kk], bcast(pa[t][kk >> 1]));
+                    else da[t] = decode8(ca[t][kk], bcast(pa[t][kk >> 1]));
                 }
 #pragma unroll
                 for (int u = 0; u < NT; ++u) {
@@ -748,18 +773,22 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     // This wave's chunks c_i = wave + i WV, i < n.  Chunks i .. i + D - 1 are in flight while
     // chunk i is computed (buffer i % D, registers R[i % D]).  Every step issues the loads
     // of chunk i + D, past the end too (they read nothing and write zeros to its own
-    // buffer), so that when a step starts exactly D - 1 chunks' loads follow its own and the
-    // wait count is the same on every path, including the compiler's own counting for the
-    // registers of each R[d].
+    // buffer).  The wait before chunk i counts only loads that are issued after chunk i's
+    // direct-to-LDS loads on every path: chunk i's own register loads (read right after the
+    // wait, and kept behind its LDS loads by issue()) and the D - 1 later chunks' LDS loads,
+    // which write memory and so stay where they are.  The later chunks' register loads do
+    // not count: the compiler may move them into the blocks that read them, so on a path
+    // that never reads them (the prologue straight to the last steps) they are not issued.
+    // The compiler waits for the registers itself.
     const int n = wave < NC ? (NC - wave + WV - 1) / WV : 0;
-    Regs<NT, MT, AR> R[D];
+    Regs<NT, MT, AR, AS> R[D];
     nv::for_each_index([&](auto d_c) {
         constexpr int d = decltype(d_c)::value;
         issue(wave + d * WV, wbuf + d * WB, R[d]);
     }, std::make_integer_sequence<int, D>{});
     auto step = [&](int i, auto d_c) __attribute__((always_inline)) {
         constexpr int d = decltype(d_c)::value;
-        wait<waitcnt_vm_lgkm0((D - 1) * LPC)>();  // chunk i's loads are done
+        wait<waitcnt_vm_lgkm0(VM)>();  // chunk i's LDS rows have landed
         pin(R[d]);
         compute(wbuf + d * WB, R[d]);
         // the loads of chunk i + D overwrite this buffer: every read of it is done
@@ -874,19 +903,23 @@ int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bi
     // activation fragments decoded in registers were 10-20% slower at M <= 8.  For M > 16 two
     // weight tiles per workgroup halve the activation decoding per weight byte, which pays
     // while N gives enough workgroups (M = 64: N = 13824 19.4 against 24.8 us with one tile;
-    // N = 5120, K = 13824 27.5 against 32.4 us with two).
+    // N = 5120, K = 13824 27.5 against 32.4 us with two).  With one tile (N < 8192) the
+    // activation codes are staged in LDS by whole-line loads rather than loaded by each lane
+    // (M = 32, N = 5120, K = 5120 10.0 against 10.4 us; M = 64, N = 3072, K = 12288 22.3
+    // against 24.7; M = 64, N = 5120, K = 13824 25.1 against 26.6); with two tiles that
+    // measured no better (19.6 against 19.5 us at M = 64, N = 13824).
     const bool two = q.N >= 8192;
-#define LAUNCH(O, B, WV, NT, MT, AR, D)                                                           \
-    hipLaunchKernelGGL((nvsk::gemm_skinny_kernel<O, B, WV, NT, MT, AR, D>),                       \
+#define LAUNCH(O, B, WV, NT, MT, AR, D, AS)                                                       \
+    hipLaunchKernelGGL((nvsk::gemm_skinny_kernel<O, B, WV, NT, MT, AR, D, AS>),                   \
                        dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
-#define BY_MT(O, B)                                            \
-    do {                                                       \
-        if (p.M <= 8) LAUNCH(O, B, 4, 1, 1, 8, 2);             \
-        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16, 2);      \
-        else if (p.M <= 32 && two) LAUNCH(O, B, 4, 2, 1, 0, 2); \
-        else if (p.M <= 32) LAUNCH(O, B, 4, 1, 1, 0, 2);       \
-        else if (two) LAUNCH(O, B, 4, 2, 2, 0, 2);             \
-        else LAUNCH(O, B, 4, 1, 2, 0, 2);                      \
+#define BY_MT(O, B)                                                \
+    do {                                                           \
+        if (p.M <= 8) LAUNCH(O, B, 4, 1, 1, 8, 2, 0);              \
+        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16, 2, 0);       \
+        else if (p.M <= 32 && two) LAUNCH(O, B, 4, 2, 1, 0, 2, 0); \
+        else if (p.M <= 32) LAUNCH(O, B, 4, 1, 1, 0, 2, 32);       \
+        else if (two) LAUNCH(O, B, 4, 2, 2, 0, 2, 0);              \
+        else LAUNCH(O, B, 4, 1, 2, 0, 2, 64);                      \
     } while (0)
 #define BY_BIAS(O)                                          \
     do {                                                    \

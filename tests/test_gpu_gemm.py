@@ -276,7 +276,7 @@ def test_scaled_mm_nvfp4_hi_first_invariance(m, hip):
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 3072), (8, 200, 288), (9, 64, 1024), (16, 1000, 3072), (17, 1000, 3072),
                                    (31, 96, 224), (32, 4096, 64), (33, 130, 5120), (40, 33, 96), (64, 512, 1056),
                                    (2, 33, 32), (48, 13824, 128), (3, 160, 1536), (20, 8200, 256), (40, 8192, 96),
-                                   (12, 40, 4096)])
+                                   (12, 40, 4096), (64, 3000, 5152), (17, 8100, 2080)])
 def test_scaled_mm_nvfp4_skinny(m, n, k, out_dtype, hip):
     """At most 64 activation rows take the skinny NVFP4 kernel (a workgroup per 32 or 64
     weight rows, K split over its waves in chunks of 256 elements, two chunks in flight per
