@@ -119,6 +119,7 @@ struct Args {
     int tiles_m, tiles_n;  // 256 x 256 tile grid
     int n_full;            // workgroups [0, n_full) compute full tiles 0 .. n_full-1 (linear, grouped order)
     int n_half;            // workgroups n_full + 2 i, +1 compute the two column halves of tile n_full + i
+    int n_pref;            // the workgroups after those read the weight ahead (prefetch_weight)
     // per-tensor mode only: the two fp32 tensor scales (device), applied in the epilogue
     const float* tsa;
     const float* tsb;
@@ -584,18 +585,81 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     }
 }
 
+// A grid of one round (fewer tiles than CUs) leaves CUs idle, and its tiles wait on HBM
+// for every weight byte: the weight streams through once, and a tile's loads run only a
+// few stages ahead of its MFMAs.  Workgroups on the idle CUs (one per CU: the tile
+// kernel's LDS fills a CU) therefore read the weight ahead of the tiles, so that the
+// tiles' own loads find it in the memory-side cache (256 MB): first the weight's scale
+// words, then its codes from K byte kPrefSkip on (the tiles' prologue loads the bytes
+// before that itself) in pieces of kPiece bytes, one K range of every row, then the next
+// range, in the order the tiles consume them.  A wave loads a piece with one 16-byte load
+// per lane (8 whole lines per instruction) and discards it; the waves of the n_pref
+// workgroups take kPrefBatch consecutive pieces each in turn, so that together they
+// sweep the ranges in K order.  The loads stay inside the operands (a piece past the end
+// of a row reads nothing).  Measured (graph-timed, rotated operands, same process):
+// 256 x 18432 x 3072 31.8 -> 30.3 us, 512 x 18432 x 3072 41.3 -> 39.6, 1024 x 3072 x 3072
+// 21.7 -> 21.5.  The gain is bounded by what the cache gives at all: with the weight
+// read completely beforehand by a separate grid, the 256-row GEMM still took 27.9 us
+// against 32.0 cold and 22.4 with the same operands as the call before.  Loading one
+// dword per 64-byte sector instead, or 256-byte K ranges, measured the same or slower.
+constexpr int kPiece = 1024;
+constexpr int kPrefSkip = 4 * BK;
+constexpr int kPrefBatch = 32;
+
+template <bool UNIT>
+__device__ __forceinline__ void prefetch_weight(const Args& p, int w) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t gw = static_cast<uint32_t>(w) * (NT / 64) + (threadIdx.x >> 6);  // wave among all
+    const uint32_t stride = static_cast<uint32_t>(p.n_pref) * (NT / 64) * kPrefBatch;
+    v4u x = {0u, 0u, 0u, 0u};
+    if constexpr (!UNIT) {
+        const uint32_t sb_bytes = static_cast<uint32_t>(p.sb_rows) * p.ncb * 4;
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(p.sb, sb_bytes);
+        const uint32_t pieces = (sb_bytes + kPiece - 1) / kPiece;
+        for (uint32_t base = gw * kPrefBatch; base < pieces; base += stride) {
+            v4u v[kPrefBatch];
+#pragma unroll
+            for (int j = 0; j < kPrefBatch; ++j)
+                v[j] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rs, (base + j) * kPiece + lane * 16u, 0, 0));
+#pragma unroll
+            for (int j = 0; j < kPrefBatch; ++j) x ^= v[j];
+        }
+    }
+    const uint32_t Kb = static_cast<uint32_t>(p.K);  // code bytes per weight row
+    const uint32_t N = static_cast<uint32_t>(p.N);
+    const uint32_t ranges = Kb > kPrefSkip ? (Kb - kPrefSkip + kPiece - 1) / kPiece : 0;
+    const uint32_t pieces = ranges * N;
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(p.b, N * Kb);
+    for (uint32_t base = gw * kPrefBatch; base < pieces; base += stride) {
+        v4u v[kPrefBatch];
+#pragma unroll
+        for (int j = 0; j < kPrefBatch; ++j) {
+            const uint32_t q = base + j;
+            const uint32_t c = q / N, n = q - c * N;
+            const uint32_t k = kPrefSkip + c * kPiece + lane * 16u;
+            const uint32_t off = q < pieces && k < Kb ? n * Kb + k : 0x80000000u;
+            v[j] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < kPrefBatch; ++j) x ^= v[j];
+    }
+    __asm__ volatile("" ::"v"(x));  // the loads are kept; their values are not used
+}
+
 // One grid runs both kinds of workgroup: the full tiles first, then (when the last
 // round of full tiles would be at most half full) that round's tiles as half tiles.
 // The dispatcher starts half-tile workgroups on CUs as their last full tile ends, so
 // the tail overlaps the uneven end of the previous round instead of waiting for a
-// second launch.
+// second launch.  A grid of one round ends with the weight-prefetch workgroups.
 template <int OUT, int BIAS, bool UNIT>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
     const int b = blockIdx.x;
     if (b < p.n_full) gemm_tile<OUT, BIAS, UNIT, 4>(p, b, lds01, lds23);
-    else gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
+    else if (b < p.n_full + 2 * p.n_half) gemm_tile<OUT, BIAS, UNIT, 2>(p, b - p.n_full, lds01, lds23);
+    else prefetch_weight<UNIT>(p, b - p.n_full - 2 * p.n_half);
 }
 
 // Split-K, first launch: each workgroup one K range of one 256 x 256 tile, partial sums to
@@ -1066,7 +1130,8 @@ void launch_split(mx::Args p, int out_code, int bias_code, bool has_bias, hipStr
 
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
 // half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
-// half tiles (about 55% of a full tile's time each), in the same grid.  Activations of at
+// half tiles (about 55% of a full tile's time each), in the same grid.  A grid of one
+// round fills the remaining CUs with weight-prefetch workgroups (prefetch_weight).  Activations of at
 // most kSkinnyMaxM rows take the skinny kernel, and small grids split K when the caller
 // gives a workspace.
 template <bool UNIT>
@@ -1088,7 +1153,9 @@ int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, void* wo
     const int tail = tiles > kGemmSlots ? tiles % kGemmSlots : tiles;
     p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
     p.n_full = tiles - p.n_half;
-    launch_grid<UNIT>(p, static_cast<unsigned>(p.n_full + 2 * p.n_half), out_code, bias_code, has_bias, st);
+    const int wgs = p.n_full + 2 * p.n_half;
+    p.n_pref = wgs < kGemmSlots ? kGemmSlots - wgs : 0;
+    launch_grid<UNIT>(p, static_cast<unsigned>(wgs + p.n_pref), out_code, bias_code, has_bias, st);
     return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }
 

@@ -43,6 +43,23 @@ def test_scaled_mm_mxfp8_vs_oracle(m, n, k, out_dtype, hip):
     assert rel_l2(got, want) <= REL_L2[out_dtype]
 
 
+def test_scaled_mm_one_round_grid_with_weight_prefetch(hip):
+    """256 x 18432 x 3072 runs as 144 half tiles, and the other 112 CUs run workgroups that
+    read the weight ahead of the tiles (they write nothing): MXFP8 and per-tensor FP8
+    against the oracle on the first and last 1024 output columns (swizzled scale rows of
+    whole 128-row blocks slice like the weight)."""
+    m, n, k = 256, 18432, 3072
+    qx, sx, qw, sw = mx_operands(m, n, k, seed=77)
+    got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=torch.bfloat16).cpu()
+    ta, tb = torch.tensor([0.5]), torch.tensor([3e-3])
+    got8 = ck.scaled_mm_fp8(qx.cuda(), qw.cuda(), ta.cuda(), tb.cuda(), out_dtype=torch.bfloat16).cpu()
+    for cols in (slice(0, 1024), slice(n - 1024, n)):
+        want = ref.scaled_mm_mxfp8_ref(qx, qw[cols], sx, sw[cols], out_dtype=torch.float32)
+        assert rel_l2(got[:, cols], want) <= REL_L2[torch.bfloat16]
+        want8 = (qx.float() @ qw[cols].float().t()) * (ta * tb)
+        assert rel_l2(got8[:, cols], want8) <= REL_L2[torch.bfloat16]
+
+
 @pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_scaled_mm_mxfp8_bias(bias_dtype, hip):
     qx, sx, qw, sw = mx_operands(192, 384, 512, seed=5)
