@@ -307,6 +307,22 @@ def test_scaled_mm_nvfp4_skinny(m, n, k, out_dtype, hip):
     assert rel_l2(got, want) <= REL_L2[out_dtype]
 
 
+@pytest.mark.parametrize("k", [224, 1280, 2304, 2336])
+@pytest.mark.parametrize("n", [96, 8200])
+@pytest.mark.parametrize("m", [1, 8, 16, 24, 32, 48, 64])
+def test_scaled_mm_nvfp4_skinny_chunks_per_wave(m, n, k, hip):
+    """Every skinny configuration (by M, and one or two weight tiles by N) with 1, 5, 9 and
+    10 chunks of 256 elements, i.e. 4 waves holding 0 to 3 chunks each: the paths from the
+    prologue straight to the last step, through one loop iteration, and through the loop
+    and the last step.  Each step's wait must cover its own chunk's LDS rows on every one of
+    them (the staged activation rows included)."""
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=m * 31 + n + k)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(),
+                             out_dtype=torch.float32)
+    assert rel_l2(got, want) <= REL_L2[torch.float32]
+
+
 @pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float32, torch.float16])
 @pytest.mark.parametrize("m", [1, 12, 20, 40])
 def test_scaled_mm_nvfp4_skinny_bias_and_alpha(bias_dtype, m, hip):
