@@ -611,8 +611,8 @@ __device__ __forceinline__ v2h bcast(_Float16 x) { return v2h{x, x}; }
 // D: chunks in flight per wave (LDS weight buffers).
 // AS (AR = 0): activation rows (32 MT) whose codes are staged in LDS with the weight rows by
 // whole-line loads, or 0: each lane loads its own 16-byte code pieces.
-template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D, int AS = 0>
-__global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
+template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D, int AS>
+__device__ __forceinline__ void skinny_tile(const Args& p) {
     static_assert(AR == 0 || (MT == 1 && AR % 8 == 0 && AR <= 16), "decoded activation: 8 or 16 rows");
     static_assert(AS == 0 || (AR == 0 && AS == 32 * MT), "staged activation codes: whole tiles");
     static_assert(16 % WV == 0, "each wave stores 16 / WV accumulator registers");
@@ -854,6 +854,21 @@ __global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
     }
 }
 
+template <int OUT, int BIAS, int WV, int NT, int MT, int AR, int D, int AS>
+__global__ __launch_bounds__(64 * WV) void gemm_skinny_kernel(Args p) {
+    skinny_tile<OUT, BIAS, WV, NT, MT, AR, D, AS>(p);
+}
+
+// Eight waves share the SIMDs in pairs (the LDS holds one such workgroup per CU), so each
+// wave may have half the register file; left to that budget the compiler spends all 256
+// registers (the four-wave form needs fewer than 100) and spills some.  A limit of 128
+// keeps it in registers: the attribute's count is doubled on this architecture (one file
+// holds a wave's vector and accumulation registers), so 64 asks for 128.
+template <int OUT, int BIAS, int NT, int MT, int AR, int D, int AS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_num_vgpr(64))) void gemm_skinny_kernel8(Args p) {
+    skinny_tile<OUT, BIAS, 8, NT, MT, AR, D, AS>(p);
+}
+
 }  // namespace nvsk
 }  // namespace ckh
 
@@ -900,7 +915,11 @@ int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bi
     // Per activation size: waves per workgroup, weight tiles per workgroup, activation tiles,
     // activation rows decoded to LDS, chunks in flight per wave.  Measured (graph-timed, K = 5120,
     // N = 13824): M = 1 12.5 us, M = 8 13.0 us, M = 16 16.0 us; 8 waves, 3 chunks in flight, or
-    // activation fragments decoded in registers were 10-20% slower at M <= 8.  For M > 16 two
+    // activation fragments decoded in registers were 10-20% slower at M <= 8.  With fewer than
+    // 256 workgroups (N < 8192) 8 waves per workgroup pay instead (same process, against 4):
+    // M = 16, N = 5120, K = 13824 18.8 against 22.1 us; M = 16, N = 3072, K = 12288 17.0
+    // against 20.0; M = 1, N = 5120, K = 5120 8.1 against 8.8 (for the staged 32-row
+    // activation 8 waves measured 9-11% slower).  For M > 16 two
     // weight tiles per workgroup halve the activation decoding per weight byte, which pays
     // while N gives enough workgroups (M = 64: N = 13824 19.4 against 24.8 us with one tile;
     // N = 5120, K = 13824 27.5 against 32.4 us with two).  With one tile (N < 8192) the
@@ -910,12 +929,20 @@ int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bi
     // measured no better (19.6 against 19.5 us at M = 64, N = 13824).
     const bool two = q.N >= 8192;
 #define LAUNCH(O, B, WV, NT, MT, AR, D, AS)                                                       \
-    hipLaunchKernelGGL((nvsk::gemm_skinny_kernel<O, B, WV, NT, MT, AR, D, AS>),                   \
-                       dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
+    do {                                                                                          \
+        if constexpr (WV == 8)                                                                    \
+            hipLaunchKernelGGL((nvsk::gemm_skinny_kernel8<O, B, NT, MT, AR, D, AS>),              \
+                               dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(512), 0, st, p); \
+        else                                                                                      \
+            hipLaunchKernelGGL((nvsk::gemm_skinny_kernel<O, B, WV, NT, MT, AR, D, AS>),           \
+                               dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p); \
+    } while (0)
 #define BY_MT(O, B)                                                \
     do {                                                           \
-        if (p.M <= 8) LAUNCH(O, B, 4, 1, 1, 8, 2, 0);              \
-        else if (p.M <= 16) LAUNCH(O, B, 4, 1, 1, 16, 2, 0);       \
+        if (p.M <= 8 && two) LAUNCH(O, B, 4, 1, 1, 8, 2, 0);       \
+        else if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8, 2, 0);         \
+        else if (p.M <= 16 && two) LAUNCH(O, B, 4, 1, 1, 16, 2, 0); \
+        else if (p.M <= 16) LAUNCH(O, B, 8, 1, 1, 16, 2, 0);       \
         else if (p.M <= 32 && two) LAUNCH(O, B, 4, 2, 1, 0, 2, 0); \
         else if (p.M <= 32) LAUNCH(O, B, 4, 1, 1, 0, 2, 32);       \
         else if (two) LAUNCH(O, B, 4, 2, 2, 0, 2, 0);              \
