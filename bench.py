@@ -341,11 +341,13 @@ LINEAR_SHAPES = [
     ("wan_attn", 8192, 5120, 5120), ("wan_ffn_up", 8192, 13824, 5120), ("wan_ffn_down", 8192, 5120, 13824),
     # short activations (e.g. a text prompt's tokens): small tile grids, split-K or half tiles
     ("m256_flux_mod", 256, 18432, 3072), ("m256_wan_ffn_up", 256, 13824, 5120), ("m256_wan_ffn_down", 256, 5120, 13824),
+    ("m64_flux_mod", 64, 18432, 3072),
 ]
 # NVFP4 linears (no vendor NVFP4 GEMM on this stack): skinny, split-K and full tile grids
 NV_LINEAR_SHAPES = [
     ("wan_ffn_up_m1", 1, 13824, 5120), ("wan_ffn_up_m16", 16, 13824, 5120), ("wan_ffn_up_m64", 64, 13824, 5120),
     ("wan_ffn_up_m256", 256, 13824, 5120), ("wan_ffn_down_m256", 256, 5120, 13824), ("flux_mod_m1", 1, 18432, 3072),
+    ("wan_ffn_down_m16", 16, 5120, 13824), ("wan_ffn_down_m64", 64, 5120, 13824),
 ]
 
 

@@ -295,12 +295,11 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     constexpr int TBN = 64 * NW;  // tile width along n
     constexpr int PB = TBN / 32;  // staged weight loads per lane per pair of stages
     constexpr int SLOTS = 4 * NW;  // MFMAs per wave per stage
-    static_assert(!SPLIT || NW == 4, "split-K runs full tiles");
 
     // Workgroups are dispatched round-robin over the 8 XCDs; full tiles are remapped so
     // each XCD walks a contiguous range of tiles (in grouped order).  Half tiles give
     // tile L's two column halves to consecutive workgroups.  Split-K workgroups take tile
-    // bid / splits, K range bid % splits.
+    // (or half tile) bid / splits, K range bid % splits.
     const int KT = (p.K + BK - 1) / BK;
     const int split = SPLIT ? bid % p.splits : 0;
     if (SPLIT) bid /= p.splits;
@@ -311,7 +310,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     const int t1 = SPLIT ? min(t0 + p.ks, KT) : KT;
     const int kend = SPLIT ? min(t1 * BK, p.K) : p.K;
     const int pend = SPLIT ? min(p.ncb, (t1 + 1) / 2) : p.ncb;
-    const int L = (NW == 4) ? bid : p.n_full + (bid >> 1);
+    const int L = (NW == 4) ? bid : (SPLIT ? 0 : p.n_full) + (bid >> 1);
     int tm, tn;
     grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
@@ -486,13 +485,14 @@ __device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds01
     if constexpr (SPLIT) {
         __builtin_amdgcn_s_waitcnt(0);  // prefetches past this range (zeros) have landed
         // The raw fp32 accumulators go to the workspace in register order: float4 g of
-        // MFMA tile (i, j) of wave w, lane l at ((w * 16 + 4 i + j) * 4 + g) * 64 + l, so
+        // MFMA tile (i, j) of wave w, lane l at ((w * 4 NW + 4 i + j) * 4 + g) * 64 + l, so
         // every store instruction writes 1 KB contiguously.  The reduce kernel adds the
         // splits and runs the epilogue.
-        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPartTile / 4) +
-                      wave * 4096 + lane;
+        constexpr int kPart = BM * TBN;  // fp32 values of one partial (half) tile
+        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPart / 4) +
+                      wave * (kPart / 16) + lane;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NW; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -662,31 +662,36 @@ __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     else prefetch_weight<UNIT>(p, b - p.n_full - 2 * p.n_half);
 }
 
-// Split-K, first launch: each workgroup one K range of one 256 x 256 tile, partial sums to
-// the workspace (no output, bias or tensor scale here).
-template <bool UNIT>
+// Split-K, first launch: each workgroup one K range of one 256 x 256 tile (NW = 4) or
+// 256 x 128 half tile (NW = 2), partial sums to the workspace (no output, bias or tensor
+// scale here).
+template <bool UNIT, int NW>
 __global__ __launch_bounds__(NT) void gemm_split_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds01[2 * BUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds23[2 * BUF];
-    gemm_tile<CKH_F32, -1, UNIT, 4, true>(p, blockIdx.x, lds01, lds23);
+    gemm_tile<CKH_F32, -1, UNIT, NW, true>(p, blockIdx.x, lds01, lds23);
 }
 
-// Split-K, second launch: thread q adds float4 q % 16384 of tile q / 16384 over the splits
-// in split order (the sum does not depend on which workgroup finished first), then applies
-// the tensor scale and bias and stores out[m][n .. n + 3] (the register mapping of the tile
-// kernel's epilogue).
-template <int OUT, int BIAS, bool UNIT>
+// Split-K, second launch: thread q adds float4 q % U of unit q / U (U = 4096 NW float4 of a
+// tile or half tile) over the splits in split order (the sum does not depend on which
+// workgroup finished first), then applies the tensor scale and bias and stores
+// out[m][n .. n + 3] (the register mapping of the tile kernel's epilogue).
+template <int OUT, int BIAS, bool UNIT, int NW>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
+    constexpr int kUnit = BM * 64 * NW / 4;  // float4 of one partial (half) tile
+    constexpr int kLog = NW == 4 ? 14 : 13;
+    static_assert(kUnit == 1 << kLog, "unit size");
     const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int L = static_cast<int>(q >> 14);
-    if (L >= p.tiles_m * p.tiles_n) return;
-    const int rest = static_cast<int>(q & 16383);
-    const int wave = rest >> 12, ij = (rest >> 8) & 15, g = (rest >> 6) & 3, lane = rest & 63;
+    const int U = static_cast<int>(q >> kLog);
+    if (U >= p.tiles_m * p.tiles_n * (4 / NW)) return;
+    const int rest = static_cast<int>(q & (kUnit - 1));
+    const int wave = rest >> (kLog - 2), ij = (rest >> 8) & (4 * NW - 1), g = (rest >> 6) & 3, lane = rest & 63;
     const int i = ij >> 2, j = ij & 3;
-    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(L) * p.splits * (kPartTile / 4) + rest;
+    const int L = NW == 4 ? U : U >> 1;
+    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(U) * p.splits * kUnit + rest;
     float4 v = src[0];
     for (int s = 1; s < p.splits; ++s) {
-        const float4 w = src[static_cast<int64_t>(s) * (kPartTile / 4)];
+        const float4 w = src[static_cast<int64_t>(s) * kUnit];
         v.x += w.x;
         v.y += w.y;
         v.z += w.z;
@@ -695,7 +700,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
     int tm, tn;
     grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m = tm * BM + (wave & 1) * 128 + j * 32 + (lane & 31);
-    const int n = tn * BN + (wave >> 1) * 128 + i * 32 + 8 * g + 4 * (lane >> 5);
+    const int n = tn * BN + (NW == 4 ? 0 : (U & 1) * 128) + (wave >> 1) * 32 * NW + i * 32 + 8 * g + 4 * (lane >> 5);
     if (m >= p.M || n >= p.N) return;
     float o[4] = {v.x, v.y, v.z, v.w};
     const float alpha = UNIT ? p.tsa[0] * p.tsb[0] : 1.0f;
@@ -1081,39 +1086,54 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
 // workgroups, at most one per CU, which write fp32 partial tiles to the caller's workspace;
 // a second launch adds them.  A partial tile (256 KB) costs about as much memory traffic
 // to write and again to read back as 8 stages of operand loads, so short K (fewer than
-// kMinSplitK stages) keeps whole-K half tiles instead.  Measured, graph-timed: M = 256,
-// N = 5120, K = 13824 40.5 against 110.8 us (half tiles); N = 13824, K = 5120 40.1 against
-// 46.9 us; N = 18432, K = 3072 38.3 against 32.1 us (not split).  Returns S (1: no split)
-// and sets ks.
+// kMinSplitK stages) keeps whole-K half tiles instead.  With at most a quarter as many
+// tiles as CUs the split runs 256 x 128 half tiles, at least two K ranges each: a half
+// tile's stage costs ~53% of a full tile's (C4's last round) and its partial (128 KB) half
+// as much traffic, so for the same workgroups the partials move half the bytes.
+// Measured, graph-timed: M = 256, N = 5120, K = 13824 40.5 us split in full tiles against
+// 110.8 us whole-K half tiles; N = 13824, K = 5120 40.1 against 46.9 us; N = 18432,
+// K = 3072 38.3 against 32.1 us (not split).  Half tiles against full tiles in the split
+// (same process): 256 x 4096 x 4096 20.9 against 27.1 us, 256 x 5120 x 13824 36.3 against
+// 40.4, 512 x 3072 x 13824 38.6 against 42.5, 256 x 13824 x 5120 38.7 against 40.6.
 constexpr int kMinSplitStages = 12;
 constexpr int kMinSplitK = 64;  // stages
 
-int split_count(int M, int N, int K, int& ks) {
-    ks = 0;
-    if (M <= kSkinnyMaxM) return 1;
+struct SplitPlan {
+    int S = 1;   // K ranges (1: no split)
+    int ks = 0;  // stages per range
+    int nw = 4;  // 4: full tiles, 2: half tiles
+};
+
+SplitPlan split_plan(int M, int N, int K) {
+    SplitPlan sp;
+    if (M <= kSkinnyMaxM) return sp;
     const int tiles = static_cast<int>(cdiv(M, mx::BM) * cdiv(N, mx::BN));
     const int KT = static_cast<int>(cdiv(K, mx::BK));
-    if (tiles > kGemmSlots / 2 || KT < kMinSplitK) return 1;
-    const int S = min(kGemmSlots / tiles, KT / kMinSplitStages);
-    if (S < 2) return 1;
-    ks = static_cast<int>(rup(cdiv(KT, S), 4));
-    return static_cast<int>(cdiv(KT, ks));
+    if (tiles > kGemmSlots / 2 || KT < kMinSplitK) return sp;
+    const bool half = tiles <= kGemmSlots / 4;
+    const int units = half ? 2 * tiles : tiles;
+    const int S = min(kGemmSlots / units, KT / kMinSplitStages);
+    if (S < 2) return sp;
+    sp.ks = static_cast<int>(rup(cdiv(KT, S), 4));
+    sp.S = static_cast<int>(cdiv(KT, sp.ks));
+    sp.nw = half ? 2 : 4;
+    return sp;
 }
 
+// one partial tile (or two partial half tiles) per tile and K range
 int64_t split_workspace_bytes(int M, int N, int K) {
-    int ks;
-    const int S = split_count(M, N, K, ks);
-    if (S < 2) return 0;
-    return cdiv(M, mx::BM) * cdiv(N, mx::BN) * S * static_cast<int64_t>(mx::kPartTile) * 4;
+    const SplitPlan sp = split_plan(M, N, K);
+    if (sp.S < 2) return 0;
+    return cdiv(M, mx::BM) * cdiv(N, mx::BN) * sp.S * static_cast<int64_t>(mx::kPartTile) * 4;
 }
 
-template <bool UNIT>
+template <bool UNIT, int NW>
 void launch_split(mx::Args p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
-    const int tiles = p.tiles_m * p.tiles_n;
-    hipLaunchKernelGGL((mx::gemm_split_kernel<UNIT>), dim3(static_cast<unsigned>(tiles * p.splits)), dim3(mx::NT), 0,
-                       st, p);
-    const dim3 g2(static_cast<unsigned>(tiles * (mx::kPartTile / 4 / 256)));
-#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_reduce_kernel<O, B, UNIT>), g2, dim3(256), 0, st, p)
+    const int units = p.tiles_m * p.tiles_n * (4 / NW);
+    hipLaunchKernelGGL((mx::gemm_split_kernel<UNIT, NW>), dim3(static_cast<unsigned>(units * p.splits)),
+                       dim3(mx::NT), 0, st, p);
+    const dim3 g2(static_cast<unsigned>(units * (mx::BM * 64 * NW / 4 / 256)));
+#define LAUNCH(O, B) hipLaunchKernelGGL((mx::gemm_reduce_kernel<O, B, UNIT, NW>), g2, dim3(256), 0, st, p)
 #define BY_BIAS(O)                                                     \
     do {                                                               \
         if (!has_bias) LAUNCH(O, -1);                                  \
@@ -1131,20 +1151,20 @@ void launch_split(mx::Args p, int out_code, int bias_code, bool has_bias, hipStr
 // The 256 x 256 tiles run one per CU in rounds.  When the last round would be at most
 // half full (e.g. 864 tiles = 3 rounds + 96), its tiles run as twice as many 256 x 128
 // half tiles (about 55% of a full tile's time each), in the same grid.  A grid of one
-// round fills the remaining CUs with weight-prefetch workgroups (prefetch_weight).  Activations of at
-// most kSkinnyMaxM rows take the skinny kernel, and small grids split K when the caller
-// gives a workspace.
+// round fills the remaining CUs with weight-prefetch workgroups (prefetch_weight).
+// Activations of at most kSkinnyMaxM rows take the skinny kernel, and small grids split K
+// when the caller gives a workspace.
 template <bool UNIT>
 int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, void* workspace, int64_t workspace_bytes,
                 hipStream_t st) {
     if (p.M <= kSkinnyMaxM) return launch_skinny<UNIT>(p, out_code, bias_code, has_bias, st);
-    int ks;
-    const int S = split_count(p.M, p.N, p.K, ks);
-    if (S > 1 && workspace && workspace_bytes >= split_workspace_bytes(p.M, p.N, p.K)) {
-        p.splits = S;
-        p.ks = ks;
+    const SplitPlan sp = split_plan(p.M, p.N, p.K);
+    if (sp.S > 1 && workspace && workspace_bytes >= split_workspace_bytes(p.M, p.N, p.K)) {
+        p.splits = sp.S;
+        p.ks = sp.ks;
         p.part = static_cast<float*>(workspace);
-        launch_split<UNIT>(p, out_code, bias_code, has_bias, st);
+        if (sp.nw == 2) launch_split<UNIT, 2>(p, out_code, bias_code, has_bias, st);
+        else launch_split<UNIT, 4>(p, out_code, bias_code, has_bias, st);
         return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
     }
     const int tiles = p.tiles_m * p.tiles_n;

@@ -142,10 +142,11 @@ int ckh_apply_rope(const void* xq, const void* xk, const void* freqs, void* xq_o
 /*
  * Bytes of device workspace ckh_scaled_mm_mxfp8 / ckh_scaled_mm_fp8 use at this shape to
  * split K (0: the shape does not split).  A grid of at most 128 output tiles of 256 x 256
- * (e.g. M = 256, N = 18432) splits K over up to 256 workgroups, which write fp32 partial
- * tiles (256 KB each) to the workspace; a second launch adds them in a fixed order and
- * applies scale, bias and output rounding.  No counterpart in the reference (torch's
- * scaled_mm takes no workspace).
+ * with K > 4032 (64 stages of 64; e.g. M = 256, N = 13824, K = 5120) splits K over up to 256
+ * workgroups, which write fp32 partial tiles (256 KB each; grids of at most 64 tiles split
+ * 256 x 128 half tiles, 128 KB each) to the workspace; a second launch adds them in a
+ * fixed order and applies scale, bias and output rounding.  No counterpart in the
+ * reference (torch's scaled_mm takes no workspace).
  */
 int64_t ckh_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 

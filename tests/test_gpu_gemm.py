@@ -219,12 +219,14 @@ def test_scaled_mm_split_k_bias_and_per_tensor(bias_dtype, hip):
 
 
 def test_scaled_mm_workspace_bytes(hip):
-    """Only small tile grids with enough K split; big grids, skinny M and short K do not."""
+    """Only small tile grids with enough K split; big grids, skinny M and short K do not.
+    At most 64 tiles split as half tiles (two 128 KB partials per tile and K range)."""
     import comfy_kitchen.backends.hip as hb
 
     f = hb._lib.ckh_scaled_mm_workspace_bytes
-    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 80 stages: 4 ranges of 20
-    assert f(256, 5120, 13824) == 20 * 11 * 256 * 256 * 4  # 216 stages: 11 ranges of 20
+    assert f(256, 13824, 5120) == 54 * 2 * 256 * 256 * 4  # 108 half tiles, 80 stages: 2 ranges of 40
+    assert f(256, 5120, 13824) == 20 * 6 * 256 * 256 * 4  # 40 half tiles, 216 stages: 6 ranges of 36
+    assert f(256, 32768, 5120) == 128 * 2 * 256 * 256 * 4  # 128 full tiles: 2 ranges of 40
     assert f(4608, 12288, 13824) == 0  # 864 tiles
     assert f(64, 18432, 13824) == 0  # skinny kernel
     assert f(256, 18432, 3072) == 0  # 48 stages: whole-K half tiles
