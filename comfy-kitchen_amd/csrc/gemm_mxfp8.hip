@@ -1089,14 +1089,21 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
 // kMinSplitK stages) keeps whole-K half tiles instead.  With at most a quarter as many
 // tiles as CUs the split runs 256 x 128 half tiles, at least two K ranges each: a half
 // tile's stage costs ~53% of a full tile's (C4's last round) and its partial (128 KB) half
-// as much traffic, so for the same workgroups the partials move half the bytes.
+// as much traffic, so for the same workgroups the partials move half the bytes.  Half
+// tiles split from kMinSplitKHalf stages on, and below kMinSplitK stages on at most
+// kShortSplitSlots workgroups (same process, against whole-K half tiles: 512 x 4096 x 3072
+// 23.0 against 28.5 us, 22.6 with 256 workgroups; 256 x 9216 x 3072 24.8 against 29.3;
+// 256 x 3072 x 3072 17.9 against 21.2; with that cap on long K too, 256 x 5120 x 13824
+// took 38.3 against 36.0 us).
 // Measured, graph-timed: M = 256, N = 5120, K = 13824 40.5 us split in full tiles against
 // 110.8 us whole-K half tiles; N = 13824, K = 5120 40.1 against 46.9 us; N = 18432,
 // K = 3072 38.3 against 32.1 us (not split).  Half tiles against full tiles in the split
 // (same process): 256 x 4096 x 4096 20.9 against 27.1 us, 256 x 5120 x 13824 36.3 against
 // 40.4, 512 x 3072 x 13824 38.6 against 42.5, 256 x 13824 x 5120 38.7 against 40.6.
 constexpr int kMinSplitStages = 12;
-constexpr int kMinSplitK = 64;  // stages
+constexpr int kMinSplitK = 64;      // stages
+constexpr int kMinSplitKHalf = 32;  // stages, half tiles
+constexpr int kShortSplitSlots = 224;
 
 struct SplitPlan {
     int S = 1;   // K ranges (1: no split)
@@ -1109,10 +1116,11 @@ SplitPlan split_plan(int M, int N, int K) {
     if (M <= kSkinnyMaxM) return sp;
     const int tiles = static_cast<int>(cdiv(M, mx::BM) * cdiv(N, mx::BN));
     const int KT = static_cast<int>(cdiv(K, mx::BK));
-    if (tiles > kGemmSlots / 2 || KT < kMinSplitK) return sp;
     const bool half = tiles <= kGemmSlots / 4;
+    if (tiles > kGemmSlots / 2 || KT < (half ? kMinSplitKHalf : kMinSplitK)) return sp;
     const int units = half ? 2 * tiles : tiles;
-    const int S = min(kGemmSlots / units, KT / kMinSplitStages);
+    const int slots = half && KT < kMinSplitK ? kShortSplitSlots : kGemmSlots;
+    const int S = min(slots / units, KT / kMinSplitStages);
     if (S < 2) return sp;
     sp.ks = static_cast<int>(rup(cdiv(KT, S), 4));
     sp.S = static_cast<int>(cdiv(KT, sp.ks));

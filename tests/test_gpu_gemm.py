@@ -178,7 +178,7 @@ def _mx_abi(qx, qw, sx, sw, out_dtype, ws):
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(256, 4096, 4096), (300, 2000, 4160), (129, 520, 4128), (65, 18432, 4096),
-                                   (512, 3072, 13824)])
+                                   (512, 3072, 13824), (200, 2000, 2080)])
 def test_scaled_mm_mxfp8_split_k(m, n, k, out_dtype, hip):
     """Grids of at most 128 tiles split K over more workgroups into a workspace, and a second
     launch adds the partial tiles (fixed order) and runs the epilogue: against the oracle,
@@ -227,9 +227,11 @@ def test_scaled_mm_workspace_bytes(hip):
     assert f(256, 13824, 5120) == 54 * 2 * 256 * 256 * 4  # 108 half tiles, 80 stages: 2 ranges of 40
     assert f(256, 5120, 13824) == 20 * 6 * 256 * 256 * 4  # 40 half tiles, 216 stages: 6 ranges of 36
     assert f(256, 32768, 5120) == 128 * 2 * 256 * 256 * 4  # 128 full tiles: 2 ranges of 40
+    assert f(256, 9216, 3072) == 36 * 3 * 256 * 256 * 4  # 72 half tiles, 48 stages: 3 ranges of 16
     assert f(4608, 12288, 13824) == 0  # 864 tiles
     assert f(64, 18432, 13824) == 0  # skinny kernel
-    assert f(256, 18432, 3072) == 0  # 48 stages: whole-K half tiles
+    assert f(256, 18432, 3072) == 0  # 72 tiles, 48 stages: whole-K half tiles
+    assert f(256, 4096, 1984) == 0  # 31 stages
     assert f(0, 4096, 8192) == 0 and f(256, 4096, -1) == 0
 
 
