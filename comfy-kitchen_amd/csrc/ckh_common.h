@@ -360,6 +360,19 @@ __device__ __forceinline__ float scale_of_amax_bits(uint32_t amax_bits, float in
     else return q;
 }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+inline int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
 // Raw buffer descriptor over [p, p + bytes): loads at offsets past `bytes` return 0.  The
 // inputs are wave-uniform by construction; reading them through readfirstlane keeps the
 // descriptor in SGPRs (a descriptor the compiler believes divergent turns every load into

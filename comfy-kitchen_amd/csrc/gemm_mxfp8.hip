@@ -1191,7 +1191,10 @@ int launch_gemm(mx::Args p, int out_code, int bias_code, bool has_bias, void* wo
     p.n_half = (tail > 0 && tail <= kGemmSlots / 2) ? tail : 0;
     p.n_full = tiles - p.n_half;
     const int wgs = p.n_full + 2 * p.n_half;
-    p.n_pref = wgs < kGemmSlots ? kGemmSlots - wgs : 0;
+    // (the CUs the device has, which a partitioned GPU reduces: prefetch workgroups that
+    // found no idle CU would run after the tiles, for nothing)
+    const int cus = device_cus();
+    p.n_pref = wgs < cus ? cus - wgs : 0;
     launch_grid<UNIT>(p, static_cast<unsigned>(wgs + p.n_pref), out_code, bias_code, has_bias, st);
     return check_launch(UNIT ? "scaled_mm_fp8" : "scaled_mm_mxfp8");
 }

@@ -198,19 +198,6 @@ __global__ __launch_bounds__(256) void quantize_fp8_pipe_kernel(const void* __re
     }
 }
 
-// Compute units of the current device (cached per device).
-inline int device_cus() {
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int c = 0;
-        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-        cus[dev] = c;
-    }
-    return cus[dev];
-}
-
 template <int IN>
 __device__ __forceinline__ float decode_fp8(uint32_t c) {
     return IN == CKH_E4M3 ? e4m3_to_f(c) : e5m2_to_f(c);
