@@ -228,8 +228,8 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
     const int NG = (Kb + GKB - 1) / GKB;  // groups of 256 elements
-    // this workgroup's groups [gb, ge) (gb even), the code bytes and scale-word columns they
-    // cover: loads past them read zeros
+    // this workgroup's groups [gb, ge), the code bytes and scale-word columns they cover:
+    // loads past them read zeros
     const int gb = SPLIT ? split * p.ks : 0;
     const int ge = SPLIT ? min(gb + p.ks, NG) : NG;
     const int kend = SPLIT ? min(ge * GKB, Kb) : Kb;
@@ -350,8 +350,10 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     for_each_index([&](auto i_c) { read_part(lds0, S0{}, i_c, R0); }, std::make_integer_sequence<int, 10>{});
     for_each_index([&](auto p_c) { decode_part(R0, K0{}, p_c, D0); }, std::make_integer_sequence<int, 16>{});
 
-    // groups in pairs (buffer = group % 2); groups past K are all zeros
-    for (int g = gb; g < ge; g += 2) {
+    // groups in pairs (buffer = (group - gb) % 2); an odd count ends after the first group of
+    // its last pair (the second, past the range, was loaded as zeros and is not computed)
+    int g = gb;
+    for (; g + 1 < ge; g += 2) {
         stage(G0{}, S0{}, g, R0, R1);
         stage(G0{}, S1{}, g, R1, R0);
         stage(G0{}, S2{}, g, R0, R1);
@@ -360,6 +362,12 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
         stage(G1{}, S1{}, g + 1, R1, R0);
         stage(G1{}, S2{}, g + 1, R0, R1);
         stage(G1{}, S3{}, g + 1, R1, R0);
+    }
+    if (g < ge) {
+        stage(G0{}, S0{}, g, R0, R1);
+        stage(G0{}, S1{}, g, R1, R0);
+        stage(G0{}, S2{}, g, R0, R1);
+        stage(G0{}, S3{}, g, R1, R0);
     }
     // the loads of the groups past the end still write LDS, which the epilogue reuses
     __builtin_amdgcn_s_waitcnt(0);
@@ -880,11 +888,14 @@ namespace {
 constexpr int kNvSkinnyMaxM = 64;
 
 // Split-K: a grid of at most 128 tiles (half the CUs) with at least kNvMinSplitK groups of
-// 256 elements runs S K ranges of every tile (each an even number of groups, at least
-// kNvMinSplitGroups) as S times as many workgroups, at most 256, which write fp32 partial
-// tiles to the caller's workspace; a second launch adds them.  A group costs about 4 us of
-// MFMA time per tile and a partial tile's round trip about as much as one group.  Returns
-// S (1: no split) and sets ks.
+// 256 elements runs S K ranges of every tile (each of ks groups, the last one fewer, at
+// least kNvMinSplitGroups) as S times as many workgroups, at most 256, which write fp32
+// partial tiles to the caller's workspace; a second launch adds them.  A group costs about
+// 4 us of MFMA time per tile and a partial tile's round trip about as much as one group.
+// Ranges of an odd number of groups end mid-pair (measured against ranges rounded up to an
+// even count, same process: M = 256, N = 13824, K = 5120, four ranges of 5 instead of 6, 6,
+// 6, 2: 48.7 against 53.8 us; M = 300, N = 2000, K = 4160 35.0 against 39.6; M = 2048,
+// N = 4096, K = 5376 84.6 against 90.1).  Returns S (1: no split) and sets ks.
 constexpr int kNvSlots = 256;
 constexpr int kNvMinSplitK = 8;
 constexpr int kNvMinSplitGroups = 4;
@@ -897,7 +908,7 @@ int nv_split_count(int64_t M, int64_t N, int64_t K, int& ks) {
     if (tiles > kNvSlots / 2 || NG < kNvMinSplitK) return 1;
     const int S = min(kNvSlots / tiles, NG / kNvMinSplitGroups);
     if (S < 2) return 1;
-    ks = static_cast<int>(rup(cdiv(NG, S), 2));
+    ks = static_cast<int>(cdiv(NG, S));
     return static_cast<int>(cdiv(NG, ks));
 }
 

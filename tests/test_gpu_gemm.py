@@ -359,10 +359,11 @@ def _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias=None):
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(256, 4096, 2048), (300, 2000, 4160), (129, 520, 5152), (65, 13824, 2048)])
 def test_scaled_mm_nvfp4_split_k(m, n, k, out_dtype, hip):
-    """Small NVFP4 tile grids split K into a workspace (ranges of an even number of
-    256-element groups; a last range shorter than the others, K % 256 != 0, rows past M,
-    columns past N), against the oracle and against the unsplit call (fp32 summation order
-    only); the reduce kernel applies alpha and bias."""
+    """Small NVFP4 tile grids split K into a workspace (ranges of ks 256-element groups, odd
+    counts and odd starts included, and a last range shorter than the others, down to one
+    group; K % 256 != 0, rows past M, columns past N), against the oracle and against the
+    unsplit call (fp32 summation order only; an odd group count there too); the reduce
+    kernel applies alpha and bias."""
     import comfy_kitchen.backends.hip as hb
 
     nbytes = hb._lib.ckh_scaled_mm_nvfp4_workspace_bytes(m, n, k)
@@ -384,7 +385,8 @@ def test_scaled_mm_nvfp4_workspace_bytes(hip):
     import comfy_kitchen.backends.hip as hb
 
     f = hb._lib.ckh_scaled_mm_nvfp4_workspace_bytes
-    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 20 groups: ranges of 6
+    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 20 groups: 4 ranges of 5
+    assert f(256, 5120, 13824) == 20 * 11 * 256 * 256 * 4  # 54 groups: 11 ranges of 5
     assert f(8192, 13824, 5120) == 0  # 1728 tiles
     assert f(64, 13824, 5120) == 0  # skinny kernel
     assert f(256, 13824, 1024) == 0  # 4 groups
