@@ -895,7 +895,10 @@ constexpr int kNvSkinnyMaxM = 64;
 // Ranges of an odd number of groups end mid-pair (measured against ranges rounded up to an
 // even count, same process: M = 256, N = 13824, K = 5120, four ranges of 5 instead of 6, 6,
 // 6, 2: 48.7 against 53.8 us; M = 300, N = 2000, K = 4160 35.0 against 39.6; M = 2048,
-// N = 4096, K = 5376 84.6 against 90.1).  Returns S (1: no split) and sets ks.
+// N = 4096, K = 5376 84.6 against 90.1).  Minimum range lengths of 2, 3, 6 and 8 groups
+// measured no better than 4 over six shapes (2: 300 x 2000 x 4160 30.9 against 34.4 us but
+// 256 x 3072 x 12288 36.5 against 35.4; 8: up to 40% slower).  Returns S (1: no split)
+// and sets ks.
 constexpr int kNvSlots = 256;
 constexpr int kNvMinSplitK = 8;
 constexpr int kNvMinSplitGroups = 4;
