@@ -1103,7 +1103,10 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
 // kShortSplitSlots workgroups (same process, against whole-K half tiles: 512 x 4096 x 3072
 // 23.0 against 28.5 us, 22.6 with 256 workgroups; 256 x 9216 x 3072 24.8 against 29.3;
 // 256 x 3072 x 3072 17.9 against 21.2; with that cap on long K too, 256 x 5120 x 13824
-// took 38.3 against 36.0 us).
+// took 38.3 against 36.0 us).  Full tiles split only into three ranges or more: two
+// ranges give as many workgroups as whole-K half tiles, which need no partials (same
+// process: 256 x 32768 x 5120 57.6 against 66.6 us split, 384 x 12288 x 6144 54.0 against
+// 56.2; with three, 256 x 18432 x 8192 60.7 split against 71.2).
 // Measured, graph-timed: M = 256, N = 5120, K = 13824 40.5 us split in full tiles against
 // 110.8 us whole-K half tiles; N = 13824, K = 5120 40.1 against 46.9 us; N = 18432,
 // K = 3072 38.3 against 32.1 us (not split).  Half tiles against full tiles in the split
@@ -1130,7 +1133,7 @@ SplitPlan split_plan(int M, int N, int K) {
     const int units = half ? 2 * tiles : tiles;
     const int slots = half && KT < kMinSplitK ? kShortSplitSlots : kGemmSlots;
     const int S = min(slots / units, KT / kMinSplitStages);
-    if (S < 2) return sp;
+    if (S < (half ? 2 : 3)) return sp;
     sp.ks = static_cast<int>(rup(cdiv(KT, S), 4));
     sp.S = static_cast<int>(cdiv(KT, sp.ks));
     sp.nw = half ? 2 : 4;

@@ -227,7 +227,8 @@ def test_scaled_mm_workspace_bytes(hip):
     f = hb._lib.ckh_scaled_mm_workspace_bytes
     assert f(256, 13824, 5120) == 54 * 2 * 256 * 256 * 4  # 108 half tiles, 80 stages: 2 ranges of 40
     assert f(256, 5120, 13824) == 20 * 6 * 256 * 256 * 4  # 40 half tiles, 216 stages: 6 ranges of 36
-    assert f(256, 32768, 5120) == 128 * 2 * 256 * 256 * 4  # 128 full tiles: 2 ranges of 40
+    assert f(256, 32768, 5120) == 0  # 128 tiles, 2 ranges: whole-K half tiles instead
+    assert f(256, 18432, 8192) == 72 * 3 * 256 * 256 * 4  # 72 full tiles, 128 stages: 3 ranges of 44
     assert f(256, 9216, 3072) == 36 * 3 * 256 * 256 * 4  # 72 half tiles, 48 stages: 3 ranges of 16
     assert f(4608, 12288, 13824) == 0  # 864 tiles
     assert f(64, 18432, 13824) == 0  # skinny kernel
