@@ -141,12 +141,13 @@ int ckh_apply_rope(const void* xq, const void* xk, const void* freqs, void* xq_o
 
 /*
  * Bytes of device workspace ckh_scaled_mm_mxfp8 / ckh_scaled_mm_fp8 use at this shape to
- * split K (0: the shape does not split).  A grid of at most 128 output tiles of 256 x 256
- * with K > 4032 (64 stages of 64; e.g. M = 256, N = 13824, K = 5120) splits K over up to 256
- * workgroups, which write fp32 partial tiles (256 KB each; grids of at most 64 tiles split
- * 256 x 128 half tiles, 128 KB each) to the workspace; a second launch adds them in a
- * fixed order and applies scale, bias and output rounding.  No counterpart in the
- * reference (torch's scaled_mm takes no workspace).
+ * split K (0: the shape does not split).  A small grid of 256 x 256 output tiles with long
+ * K (e.g. M = 256, N = 13824, K = 5120) splits K over up to 256 workgroups, which write fp32
+ * partial tiles to the workspace: grids of at most 64 tiles as 256 x 128 half tiles
+ * (128 KB partials) from 32 stages of 64 along K, grids of 65-128 tiles as whole tiles
+ * (256 KB) from 64 stages when three ranges or more fit.  A second launch adds the
+ * partials in a fixed order and applies scale, bias and output rounding.  No counterpart
+ * in the reference (torch's scaled_mm takes no workspace).
  */
 int64_t ckh_scaled_mm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
