@@ -131,7 +131,8 @@ def test_scaled_mm_mxfp8_config4_full(hip):
                                    (2, 33, 32), (48, 18432, 128), (12, 8200, 320), (16, 4096, 3072),
                                    (20, 16400, 256), (30, 9000, 1088), (64, 16448, 320), (50, 12000, 4096),
                                    (63, 3000, 12288), (25, 160, 96), (64, 16384, 544), (36, 24576, 96),
-                                   (33, 24600, 4160)])
+                                   (33, 24600, 4160), (32, 16384, 320), (24, 18432, 544), (20, 32768, 96),
+                                   (28, 20000, 4160)])
 def test_scaled_mm_mxfp8_skinny(m, n, k, out_dtype, hip):
     """At most 64 activation rows take the skinny kernel (a workgroup per 32 or 64 weight
     rows, K split over its waves; configurations by M, boundaries 8 / 16 / 32 / 64, and from
