@@ -1054,16 +1054,19 @@ int launch_skinny(const mx::Args& q, int out_code, int bias_code, bool has_bias,
     // else 2 waves and two tiles (N = 32768: 25.2 against 29.1 and 34.5).  17-32 rows follow the
     // same rule (same process, against 4 waves and one tile): N = 16384, K = 5120 18.7 against
     // 19.8 us; M = 32, N = 18432, K = 3072 16.4 against 17.3; M = 20, N = 32768 20.2 against 22.0;
-    // at K = 12288 4 waves and one tile stay (57.4 against 57.7).  The NVFP4 skinny kernel's form
-    // (128-byte chunks, two in flight per wave) measured slower here, where a chunk costs only a
-    // few MFMAs: M = 1 14.5 against 12.9 us, M = 16 15.9 against 15.5, M = 64 29.6 against 26.5
-    // (same process).
+    // at K = 12288 4 waves and one tile stay (57.4 against 57.7).  With 4-8 rows and N above
+    // 16384, 2 waves rather than 8 (M = 8, N = 18432, K = 3072 13.4 against 14.5 us; N = 24576
+    // 14.9 against 15.8; M = 4 13.1 against 13.6; M = 1 and 2 and N = 16384 equal).  The NVFP4
+    // skinny kernel's form (128-byte chunks, two in flight per wave) measured slower here, where a
+    // chunk costs only a few MFMAs: M = 1 14.5 against 12.9 us, M = 16 15.9 against 15.5, M = 64
+    // 29.6 against 26.5 (same process).
 #define LAUNCH(O, B, WV, NT, MT, AR)                                                              \
     hipLaunchKernelGGL((mxsk::gemm_skinny_kernel<O, B, UNIT, WV, NT, MT, AR>),                    \
                        dim3(static_cast<unsigned>(cdiv(q.N, 32 * NT))), dim3(64 * WV), 0, st, p)
 #define BY_MT(O, B)                                    \
     do {                                               \
-        if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);                        \
+        if (p.M <= 8 && p.M >= 4 && p.N > 16384) LAUNCH(O, B, 2, 1, 1, 8); \
+        else if (p.M <= 8) LAUNCH(O, B, 8, 1, 1, 8);                   \
         else if (p.M <= 16 && p.N >= 8192) LAUNCH(O, B, 2, 1, 1, 16);  \
         else if (p.M <= 16 && p.N >= 4096) LAUNCH(O, B, 4, 1, 1, 16);  \
         else if (p.M <= 16) LAUNCH(O, B, 8, 1, 1, 16);                 \

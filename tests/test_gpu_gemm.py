@@ -132,7 +132,7 @@ def test_scaled_mm_mxfp8_config4_full(hip):
                                    (20, 16400, 256), (30, 9000, 1088), (64, 16448, 320), (50, 12000, 4096),
                                    (63, 3000, 12288), (25, 160, 96), (64, 16384, 544), (36, 24576, 96),
                                    (33, 24600, 4160), (32, 16384, 320), (24, 18432, 544), (20, 32768, 96),
-                                   (28, 20000, 4160)])
+                                   (28, 20000, 4160), (6, 18440, 288), (4, 24576, 3104)])
 def test_scaled_mm_mxfp8_skinny(m, n, k, out_dtype, hip):
     """At most 64 activation rows take the skinny kernel (a workgroup per 32 or 64 weight
     rows, K split over its waves; configurations by M, boundaries 8 / 16 / 32 / 64, and from
