@@ -1161,7 +1161,7 @@ def summarize_gemm(kt_dir: str, sq_dir: str, fetch_dir: str, command: str):
              "Sequence (`python3 -u bench.py --pmc-gemm-driver`): the MFMA-loop calibration, a 256 MiB negate "
              "(traffic calibration), then three calls each of " + ", ".join(f"`{o}`" for o in GEMM_OPS) +
              " on the C4 operands (A [4608, 3072], B [12288, 3072], bf16 out).", "",
-             "Commands (each a run of its own):", "", f"    {command}", "",
+             "Commands (each a run of its own):", "", *[f"    {c.strip()}" for c in command.split(";") if c.strip()], "",
              "- implied clock = SQ_BUSY_CYCLES / shader engines / duration (shader engines from the calibration "
              f"loop, whose MFMA cycles are known: {n_se:.2f}); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES "
              f"÷ the calibration's ratio ({full:.3f});",
