@@ -47,6 +47,11 @@ def test_scaled_mm_mxfp8_random_shapes(m, n, k, hip):
     got = ck.scaled_mm_mxfp8(qx.cuda(), qw.cuda(), sx.cuda(), sw.cuda(), out_dtype=out_dtype)
     assert got.shape == (m, n)
     assert rel_l2(got, want) <= REL_L2[out_dtype]
+    # the per-tensor FP8 GEMM (the same paths with unit block scales) on the same codes
+    ta, tb = torch.tensor([0.75]), torch.tensor([2e-3])
+    want8 = (qx.float() @ qw.float().t()) * (ta * tb)
+    got8 = ck.scaled_mm_fp8(qx.cuda(), qw.cuda(), ta.cuda(), tb.cuda(), out_dtype=out_dtype)
+    assert rel_l2(got8, want8) <= REL_L2[out_dtype]
 
 
 @pytest.mark.parametrize("m,n,k", _shapes(4048, 24))
