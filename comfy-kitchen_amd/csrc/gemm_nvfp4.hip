@@ -64,7 +64,9 @@ constexpr int STILE = 256 * 4 * GS;         // one operand's scale words per gro
 constexpr int GBUF = 2 * TILE + 2 * STILE;  // one group buffer: b codes, a codes, b scales, a scales
 constexpr int EPI_ROW = 520;                // bytes of one staged 16-bit output row (512 + 8 pad)
 static_assert(128 * EPI_ROW <= GBUF, "half the output tile must fit one group buffer");
-constexpr int LOADS_PER_GROUP = 18;         // per wave: 8 + 8 code loads, 2 scale loads
+// direct-to-LDS loads per wave per group of a 256 x 64 NW tile: 2 NW weight-code loads,
+// 8 activation-code loads, 2 scale loads (18 for full tiles, 14 for half tiles)
+constexpr int loads_per_group(int NW) { return 2 * NW + 8 + 2; }
 
 // fn(integral_constant<int, K>) for each K in order
 template <typename Fn, int... K>
@@ -97,19 +99,21 @@ struct Args {
     int ncb;      // scale word columns: ceil(K/16/4)
     int sa_rows, sb_rows;
     int tiles_m, tiles_n;
-    // split-K mode (gemm_split_kernel): workgroup L * splits + s computes groups
-    // [s * ks, min((s + 1) * ks, NG)) of tile L (ks even) and writes its fp32 partial tile
+    int n_full;  // workgroups [0, n_full) compute full tiles 0 .. n_full-1 (grouped order)
+    int n_half;  // workgroups n_full + 2 i, +1 compute the two column halves of tile n_full + i
+    // split-K mode (gemm_split_kernel): workgroup U * splits + s computes groups
+    // [s * ks, min((s + 1) * ks, NG)) of tile (or half tile) U and writes its fp32 partial
     int splits, ks;
     float* part;
 };
 
-// fp32 values of one partial tile in the workspace (256 x 256)
+// fp32 values of one partial tile in the workspace (256 x 256, or two 256 x 128 halves)
 constexpr int kPartTile = BM * BN;
 
 // Direct-to-LDS loads of one operand's group.  Wave w, load j (0..7) covers rows
-// R = 64 w + 8 j .. +7 (1 KB of LDS); lane i fills row R + i/8, physical chunk i%8,
-// which holds logical chunk (i%8) ^ (i/8) ^ (j & 1) (R is a multiple of 8, and bit 3
-// of the row is j's lowest bit).
+// R = 64 w + 8 j .. +7 (1 KB of LDS; 32 w + 8 j, j = 0..3, for a 128-row half tile);
+// lane i fills row R + i/8, physical chunk i%8, which holds logical chunk
+// (i%8) ^ (i/8) ^ (j & 1) (R is a multiple of 8, and bit 3 of the row is j's lowest bit).
 struct Loader {
     __amdgpu_buffer_rsrc_t rs;
     uint32_t voff;     // lane's byte offset for j = 0 and group 0
@@ -118,10 +122,11 @@ struct Loader {
     uint32_t rowstep;  // 8 rows
 };
 
-__device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int Kb, int wave, int lane) {
+__device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int valid_rows, int Kb, int wave, int lane,
+                                             int rows_per_wave = 64) {
     Loader L;
     L.rs = buffer_rsrc(tile_base, static_cast<uint32_t>(max(valid_rows, 0)) * Kb);
-    const int row = 64 * wave + (lane >> 3);
+    const int row = rows_per_wave * wave + (lane >> 3);
     L.cbyte = ((lane & 7) ^ (lane >> 3)) << 4;
     L.cdelta = static_cast<uint32_t>((L.cbyte ^ 16) - L.cbyte);
     L.voff = static_cast<uint32_t>(row * Kb + L.cbyte);
@@ -129,17 +134,20 @@ __device__ __forceinline__ Loader make_loader(const uint8_t* tile_base, int vali
     return L;
 }
 
-// Load j (0..7) of issue_codes alone.
+// Load j (0..7, or 0..3 for 32 rows per wave) of issue_codes alone.  With 32 rows per
+// wave, R = 32 w + 8 j still has bit 3 equal to j's lowest bit.
+template <int RPW = 64>
 __device__ __forceinline__ void issue_code_part(const Loader& L, uint8_t* dst, int wave, int kb0, int Kb, int j) {
     const int cb = (j & 1) ? (L.cbyte ^ 16) : L.cbyte;
     const uint32_t add = (kb0 + cb < Kb) ? static_cast<uint32_t>(kb0) : 0x80000000u;  // past K: zeros
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + (64 * wave + 8 * j) * GKB), 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(L.rs, (lds_void*)(dst + (RPW * wave + 8 * j) * GKB), 16,
                                              L.voff + j * L.rowstep + ((j & 1) ? L.cdelta : 0) + add, 0, 0, 0);
 }
 
+template <int RPW = 64>
 __device__ __forceinline__ void issue_codes(const Loader& L, uint8_t* dst, int wave, int kb0, int Kb) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) issue_code_part(L, dst, wave, kb0, Kb, j);
+    for (int j = 0; j < RPW / 8; ++j) issue_code_part<RPW>(L, dst, wave, kb0, Kb, j);
 }
 
 // Scale words of a group: for a 256-row tile, 128-row block rb and word column c, the
@@ -205,16 +213,29 @@ __device__ __forceinline__ float bias_at(const void* bias, int n) {
     else return load1<BIAS>(bias, n);
 }
 
-template <int OUT, int BIAS, bool SPLIT = false>
-__device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t* lds1) {
-    const int tiles = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
+// NW: 32-column MFMA tiles per wave along n: 4 for 256 x 256 workgroup tiles, 2 for the
+// 256 x 128 column halves of a tile (each wave 128 x 64: 8 MFMAs per substep instead of
+// 16, with 6 of the 8 operand tiles decoded).
+template <int OUT, int BIAS, int NW, bool SPLIT = false>
+__device__ __forceinline__ void gemm_tile(const Args& p, int bid, uint8_t* lds0, uint8_t* lds1) {
+    constexpr int TBN = 64 * NW;         // tile width along n
+    constexpr int RPW = TBN / 4;         // weight rows loaded per wave
+    constexpr int SLOTS = 4 * NW;        // MFMAs per wave per substep
+    constexpr int NREAD = NW + 6;        // LDS reads per wave per stage
+    constexpr int NDEC = 2 * NW + 8;     // decode parts per substep
+    constexpr int NLD = loads_per_group(NW);
+    // Workgroups are dispatched round-robin over the 8 XCDs; full tiles are remapped so
+    // each XCD walks a contiguous range of tiles (in grouped order).  Half tiles give tile
+    // L's two column halves to consecutive workgroups.  Split-K workgroups take tile (or
+    // half tile) bid / splits, K range bid % splits.
     const int split = SPLIT ? bid % p.splits : 0;
     if (SPLIT) bid /= p.splits;
-    else if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+    else if (NW == 4 && (p.n_full & 7) == 0) bid = (bid & 7) * (p.n_full >> 3) + (bid >> 3);
+    const int L = (NW == 4) ? bid : (SPLIT ? 0 : p.n_full) + (bid >> 1);
     int tm, tn;
-    grouped_tile(bid, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN + (NW == 4 ? 0 : (bid & 1) * TBN);
+    if (n0 >= p.N) return;  // a half tile wholly past N (uniform over the workgroup)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -223,7 +244,7 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     const int half = lane >> 5, r32 = lane & 31;
     const int Kb = p.K / 2;
 
-    const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * Kb, min(BN, p.N - n0), Kb, wave, lane);
+    const Loader LB = make_loader(p.b + static_cast<int64_t>(n0) * Kb, min(TBN, p.N - n0), Kb, wave, lane, RPW);
     const Loader LA = make_loader(p.a + static_cast<int64_t>(m0) * Kb, min(BM, p.M - m0), Kb, wave, lane);
     const __amdgpu_buffer_rsrc_t rssb = buffer_rsrc(p.sb, static_cast<uint32_t>(p.sb_rows) * p.ncb * 4);
     const __amdgpu_buffer_rsrc_t rssa = buffer_rsrc(p.sa, static_cast<uint32_t>(p.sa_rows) * p.ncb * 4);
@@ -235,52 +256,69 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     const int kend = SPLIT ? min(ge * GKB, Kb) : Kb;
     const int cend = SPLIT ? min(p.ncb, ge * GS) : p.ncb;
 
-    v16f acc[4][4];
+    v16f acc[NW][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NW; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v16f{};
 
     auto gbuf = [&](auto g_c) -> uint8_t* { return (decltype(g_c)::value & 1) ? lds1 : lds0; };
     auto issue_group = [&](auto g_c, int g) {
         uint8_t* d = gbuf(g_c);
-        issue_codes(LB, d, wave, g * GKB, kend);
+        issue_codes<RPW>(LB, d, wave, g * GKB, kend);
         issue_codes(LA, d + TILE, wave, g * GKB, kend);
         issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, cend, g, d + 2 * TILE, wave, lane);
     };
-    // load I (0..17) of issue_group: weight codes 0..7, activation codes 8..15, scales 16, 17
+    // load I (0..NLD-1) of issue_group: weight codes 0..2NW-1, then 8 activation codes,
+    // then the 2 scale loads (a half tile's wave also copies the scale words of the 128
+    // weight rows after its own, which it does not read, so that every wave issues the same
+    // number of loads)
     auto issue_part = [&](auto g_c, int g, auto i_c) {
         constexpr int I = decltype(i_c)::value;
         uint8_t* d = gbuf(g_c);
-        if constexpr (I < 8) issue_code_part(LB, d, wave, g * GKB, kend, I);
-        else if constexpr (I < 16) issue_code_part(LA, d + TILE, wave, g * GKB, kend, I - 8);
-        else issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, cend, g, d + 2 * TILE, wave, lane, I - 16, I - 15);
+        if constexpr (I < 2 * NW) issue_code_part<RPW>(LB, d, wave, g * GKB, kend, I);
+        else if constexpr (I < 2 * NW + 8) issue_code_part(LA, d + TILE, wave, g * GKB, kend, I - 2 * NW);
+        else issue_scales(rssb, rssa, n0 >> 7, m0 >> 7, p.ncb, cend, g, d + 2 * TILE, wave, lane, I - 2 * NW - 8,
+                          I - 2 * NW - 7);
     };
 
     // lane's fragment and scale-word addresses inside a group buffer
     const int x7 = (r32 & 7) ^ ((r32 >> 3) & 1);
-    const uint32_t frow_b = static_cast<uint32_t>((wn * 128 + r32) * GKB);
+    const uint32_t frow_b = static_cast<uint32_t>((wn * 32 * NW + r32) * GKB);
     const uint32_t frow_a = static_cast<uint32_t>(TILE + (wm * 128 + r32) * GKB);
-    const uint32_t sw_b = static_cast<uint32_t>(2 * TILE + wn * 2048 + r32 * 16);
+    // (a half tile's weight rows are one 128-row block, whose word (r % 128) / 32 is this
+    // wave's tile 2 wn + i: the two words at byte 8 wn of the lane's 16)
+    const uint32_t sw_b = static_cast<uint32_t>(2 * TILE + (NW == 4 ? wn * 2048 : 8 * wn) + r32 * 16);
     const uint32_t sw_a = static_cast<uint32_t>(2 * TILE + STILE + wm * 2048 + r32 * 16);
-    // One of the 10 LDS reads of a stage's raw operands: weight tiles 0..3, activation
-    // tiles 4..7, scale words 8, 9.
+    // One of the NREAD LDS reads of a stage's raw operands: weight tiles 0..NW-1,
+    // activation tiles NW..NW+3, scale words NW+4 (weight) and NW+5 (activation).
     auto read_part = [&](const uint8_t* gb, auto s_c, auto i_c, Raw& R) {
         constexpr int S = decltype(s_c)::value, I = decltype(i_c)::value;
         const uint32_t chunk = static_cast<uint32_t>(((2 * S + half) ^ x7) << 4);
-        if constexpr (I < 4) R.b[I] = *reinterpret_cast<const v4u*>(gb + frow_b + I * 32 * GKB + chunk);
-        else if constexpr (I < 8) R.a[I - 4] = *reinterpret_cast<const v4u*>(gb + frow_a + (I - 4) * 32 * GKB + chunk);
-        else if constexpr (I == 8) R.wb = *reinterpret_cast<const v4u*>(gb + sw_b + S * 512);
-        else R.wa = *reinterpret_cast<const v4u*>(gb + sw_a + S * 512);
+        if constexpr (I < NW) {
+            R.b[I] = *reinterpret_cast<const v4u*>(gb + frow_b + I * 32 * GKB + chunk);
+        } else if constexpr (I < NW + 4) {
+            R.a[I - NW] = *reinterpret_cast<const v4u*>(gb + frow_a + (I - NW) * 32 * GKB + chunk);
+        } else if constexpr (I == NW + 4) {
+            if constexpr (NW == 4) {
+                R.wb = *reinterpret_cast<const v4u*>(gb + sw_b + S * 512);
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(gb + sw_b + S * 512);
+                R.wb[0] = w.x;
+                R.wb[1] = w.y;
+            }
+        } else {
+            R.wa = *reinterpret_cast<const v4u*>(gb + sw_a + S * 512);
+        }
     };
     const int sh = 16 * half;
-    // Part P (0..15) of decoding substep KK of R into D (dword KK of each tile, block
-    // 2h + KK/2): half P & 1 of weight tile P / 2 (P < 8) or of activation tile P / 2 - 4,
-    // i.e. two converts and two scale multiplies.
+    // Part P (0..NDEC-1) of decoding substep KK of R into D (dword KK of each tile, block
+    // 2h + KK/2): half P & 1 of weight tile P / 2 (P < 2 NW) or of activation tile
+    // P / 2 - NW, i.e. two converts and two scale multiplies.
     auto decode_part = [&](const Raw& R, auto kk_c, auto p_c, Dec& D) {
         constexpr int KK = decltype(kk_c)::value, P = decltype(p_c)::value;
-        constexpr int t = (P >> 1) & 3, h = P & 1;
-        constexpr bool A = P >= 8;
+        constexpr bool A = P >= 2 * NW;
+        constexpr int t = A ? (P - 2 * NW) >> 1 : P >> 1, h = P & 1;
         const v2h pr = scale_pair(A ? R.wa[t] : R.wb[t], sh);
         const v2h sc = KK < 2 ? v2h{pr[0], pr[0]} : v2h{pr[1], pr[1]};
         const uint32_t w = A ? R.a[t][KK] : R.b[t][KK];
@@ -292,10 +330,12 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
         d[4 * h + 2] = e1[0];
         d[4 * h + 3] = e1[1];
     };
-    // The 16 MFMAs of one substep on Dc, each in a slot of its own with 1/16 of the decode
-    // of (Rd, KKd) into Dn and, per the flags, one LDS read of the next stage and one load
-    // of the group after next; the slots keep the decode's VALU work spread between the
-    // MFMAs (the compiler would otherwise cluster it).
+    // The SLOTS MFMAs of one substep on Dc, each in a slot of its own with its share of the
+    // decode of (Rd, KKd) into Dn (one part each for full tiles; half tiles add the last 4
+    // parts to the even slots) and, per the flags, one LDS read of the next stage and one
+    // load of the group after next (LD 1: loads 0..SLOTS-1, LD 2: the rest); the slots keep
+    // the decode's VALU work spread between the MFMAs (the compiler would otherwise cluster
+    // it).
     auto substep = [&](const Dec& Dc, const Raw& Rd, auto kkd_c, Dec& Dn, auto rd_c, const uint8_t* nb, auto sn_c,
                        Raw& Rn, auto ld_c, auto lg_c, int lg) {
         constexpr int RD = decltype(rd_c)::value, LD = decltype(ld_c)::value;
@@ -304,11 +344,13 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
             acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Dc.b[i >> 2], Dc.a[i & 3], acc[i >> 2][i & 3],
                                                                         0, 0, 0);
             decode_part(Rd, kkd_c, i_c, Dn);
-            if constexpr (RD && i < 10) read_part(nb, sn_c, i_c, Rn);
+            if constexpr (NDEC > SLOTS && (i & 1) == 0)
+                decode_part(Rd, kkd_c, std::integral_constant<int, SLOTS + i / 2>{}, Dn);
+            if constexpr (RD && i < NREAD) read_part(nb, sn_c, i_c, Rn);
             if constexpr (LD == 1) issue_part(lg_c, lg, i_c);
-            if constexpr (LD == 2 && i < 2) issue_part(lg_c, lg, std::integral_constant<int, 16 + i>{});
+            if constexpr (LD == 2 && i < NLD - SLOTS) issue_part(lg_c, lg, std::integral_constant<int, SLOTS + i>{});
             __builtin_amdgcn_sched_barrier(0);
-        }, std::make_integer_sequence<int, 16>{});
+        }, std::make_integer_sequence<int, SLOTS>{});
     };
     Raw R0, R1;
     Dec D0, D1;
@@ -346,9 +388,9 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     // prologue: groups 0 and 1 in flight, group 0 resident, stage 0 read and decoded
     issue_group(G0{}, gb);
     issue_group(G1{}, gb + 1);
-    group_barrier<waitcnt_vm_lgkm0(LOADS_PER_GROUP)>();
-    for_each_index([&](auto i_c) { read_part(lds0, S0{}, i_c, R0); }, std::make_integer_sequence<int, 10>{});
-    for_each_index([&](auto p_c) { decode_part(R0, K0{}, p_c, D0); }, std::make_integer_sequence<int, 16>{});
+    group_barrier<waitcnt_vm_lgkm0(NLD)>();
+    for_each_index([&](auto i_c) { read_part(lds0, S0{}, i_c, R0); }, std::make_integer_sequence<int, NREAD>{});
+    for_each_index([&](auto p_c) { decode_part(R0, K0{}, p_c, D0); }, std::make_integer_sequence<int, NDEC>{});
 
     // groups in pairs (buffer = (group - gb) % 2); an odd count ends after the first group of
     // its last pair (the second, past the range, was loaded as zeros and is not computed)
@@ -373,13 +415,14 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     __builtin_amdgcn_s_waitcnt(0);
     if constexpr (SPLIT) {
         // The raw fp32 accumulators go to the workspace in register order: float4 g of
-        // MFMA tile (i, j) of wave w, lane l at ((w * 16 + 4 i + j) * 4 + g) * 64 + l, so
+        // MFMA tile (i, j) of wave w, lane l at ((w * 4 NW + 4 i + j) * 4 + g) * 64 + l, so
         // every store instruction writes 1 KB contiguously.  The reduce kernel adds the
         // splits and runs the epilogue.
-        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPartTile / 4) +
-                      wave * 4096 + lane;
+        constexpr int kPart = BM * TBN;  // fp32 values of one partial (half) tile
+        float4* dst = reinterpret_cast<float4*>(p.part) + (static_cast<int64_t>(bid) * p.splits + split) * (kPart / 4) +
+                      wave * (kPart / 16) + lane;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NW; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -397,16 +440,17 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
     if constexpr (OUT != CKH_F32) {
         // Stage the 16-bit tile in LDS as 256 rows of EPI_ROW bytes (rows 0..127 in
         // buffer 0, 128..255 in buffer 1; the 520-byte pitch spreads a fragment's 32 rows
-        // over distinct bank pairs), then each wave stores 64 whole rows, 64 lanes x 8 bytes.
+        // over distinct bank pairs), then each wave stores 64 whole rows, 8 bytes per lane:
+        // one 512-byte row per instruction (full tiles) or two 256-byte rows (half tiles).
         auto row_ptr = [&](int r) -> uint8_t* { return r < 128 ? lds0 + r * EPI_ROW : lds1 + (r - 128) * EPI_ROW; };
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint8_t* rowp = row_ptr(wm * 128 + j * 32 + r32);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NW; ++i) {
 #pragma unroll
                 for (int gg = 0; gg < 4; ++gg) {
-                    const int nl = wn * 128 + i * 32 + 8 * gg + 4 * half;
+                    const int nl = wn * 32 * NW + i * 32 + 8 * gg + 4 * half;
                     const int n = n0 + nl;
                     *reinterpret_cast<uint2*>(rowp + nl * 2) =
                         make_uint2(pack2<OUT>(value(acc[i][j][4 * gg], n), value(acc[i][j][4 * gg + 1], n + 1)),
@@ -415,13 +459,16 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
             }
         }
         __syncthreads();
-        const int n = n0 + 4 * lane;
+        constexpr int LPR = TBN / 4;   // lanes per output row, 8 bytes (4 values) each
+        constexpr int RPI = 64 / LPR;  // rows per store instruction
+        const int lr = lane % LPR, lrow = lane / LPR;
+        const int n = n0 + 4 * lr;
         const bool vec = (p.N & 3) == 0 && n + 4 <= p.N;
-        const int rows = min(64, p.M - (m0 + wave * 64));
-        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64) * p.N + n;
+        const int rows = min(64, p.M - (m0 + wave * 64)) - lrow;
+        uint16_t* orow = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(m0 + wave * 64 + lrow) * p.N + n;
 #pragma unroll 8
-        for (int rl = 0; rl < 64; ++rl) {
-            const uint2 d = *reinterpret_cast<const uint2*>(row_ptr(wave * 64 + rl) + lane * 8);
+        for (int rl = 0; rl < 64; rl += RPI) {
+            const uint2 d = *reinterpret_cast<const uint2*>(row_ptr(wave * 64 + rl + lrow) + lr * 8);
             if (rl >= rows) break;
             uint16_t* o = orow + static_cast<int64_t>(rl) * p.N;
             if (vec) {
@@ -438,10 +485,10 @@ __device__ __forceinline__ void gemm_tile(const Args& p, uint8_t* lds0, uint8_t*
             const int m = m0 + wm * 128 + j * 32 + r32;
             if (m >= p.M) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NW; ++i) {
 #pragma unroll
                 for (int gg = 0; gg < 4; ++gg) {
-                    const int n = n0 + wn * 128 + i * 32 + 8 * gg + 4 * half;
+                    const int n = n0 + wn * 32 * NW + i * 32 + 8 * gg + 4 * half;
                     float v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[e] = value(acc[i][j][4 * gg + e], n + e);
@@ -463,41 +510,49 @@ template <int OUT, int BIAS>
 __global__ __launch_bounds__(NT) void gemm_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
-    gemm_tile<OUT, BIAS>(p, lds0, lds1);
+    const int b = blockIdx.x;
+    if (b < p.n_full) gemm_tile<OUT, BIAS, 4>(p, b, lds0, lds1);
+    else gemm_tile<OUT, BIAS, 2>(p, b - p.n_full, lds0, lds1);
 }
 
-// Split-K, first launch: each workgroup one K range of one tile, partial sums to the
-// workspace (alpha and bias are applied by the reduce kernel).
+// Split-K, first launch: each workgroup one K range of one 256 x 256 tile (NW = 4) or
+// 256 x 128 half tile (NW = 2), partial sums to the workspace (alpha and bias are applied
+// by the reduce kernel).
+template <int NW>
 __global__ __launch_bounds__(NT) void gemm_split_kernel(Args p) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[GBUF];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[GBUF];
-    gemm_tile<CKH_F32, -1, true>(p, lds0, lds1);
+    gemm_tile<CKH_F32, -1, NW, true>(p, blockIdx.x, lds0, lds1);
 }
 
-// Split-K, second launch: thread q adds float4 q % 16384 of tile q / 16384 over the splits
-// in split order, times alpha, plus bias, and stores out[m][n .. n + 3] (the register
-// mapping of the tile epilogue).
-template <int OUT, int BIAS>
+// Split-K, second launch: thread q adds float4 q % U of unit q / U (U = 4096 NW float4 of
+// a tile or half tile) over the splits in split order, times alpha, plus bias, and stores
+// out[m][n .. n + 3] (the register mapping of the tile epilogue).
+template <int OUT, int BIAS, int NW>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(Args p) {
+    constexpr int kUnit = BM * 64 * NW / 4;  // float4 of one partial (half) tile
+    constexpr int kLog = NW == 4 ? 14 : 13;
+    static_assert(kUnit == 1 << kLog, "unit size");
     const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    const int L = static_cast<int>(q >> 14);
-    if (L >= p.tiles_m * p.tiles_n) return;
-    const int rest = static_cast<int>(q & 16383);
-    const int wave = rest >> 12, ij = (rest >> 8) & 15, g = (rest >> 6) & 3, lane = rest & 63;
+    const int U = static_cast<int>(q >> kLog);
+    if (U >= p.tiles_m * p.tiles_n * (4 / NW)) return;
+    const int rest = static_cast<int>(q & (kUnit - 1));
+    const int wave = rest >> (kLog - 2), ij = (rest >> 8) & (4 * NW - 1), g = (rest >> 6) & 3, lane = rest & 63;
     const int i = ij >> 2, j = ij & 3;
-    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(L) * p.splits * (kPartTile / 4) + rest;
+    const float4* src = reinterpret_cast<const float4*>(p.part) + static_cast<int64_t>(U) * p.splits * kUnit + rest;
     float4 v = src[0];
     for (int s = 1; s < p.splits; ++s) {
-        const float4 w = src[static_cast<int64_t>(s) * (kPartTile / 4)];
+        const float4 w = src[static_cast<int64_t>(s) * kUnit];
         v.x += w.x;
         v.y += w.y;
         v.z += w.z;
         v.w += w.w;
     }
+    const int L = NW == 4 ? U : U >> 1;
     int tm, tn;
     grouped_tile(L, p.tiles_m, p.tiles_n, tm, tn);
     const int m = tm * BM + (wave & 1) * 128 + j * 32 + (lane & 31);
-    const int n = tn * BN + (wave >> 1) * 128 + i * 32 + 8 * g + 4 * (lane >> 5);
+    const int n = tn * BN + (NW == 4 ? 0 : (U & 1) * 128) + (wave >> 1) * 32 * NW + i * 32 + 8 * g + 4 * (lane >> 5);
     if (m >= p.M || n >= p.N) return;
     const float alpha = p.alpha[0];
     const float s4[4] = {v.x, v.y, v.z, v.w};
@@ -897,29 +952,64 @@ constexpr int kNvSkinnyMaxM = 64;
 // 6, 2: 48.7 against 53.8 us; M = 300, N = 2000, K = 4160 35.0 against 39.6; M = 2048,
 // N = 4096, K = 5376 84.6 against 90.1).  Minimum range lengths of 2, 3, 6 and 8 groups
 // measured no better than 4 over six shapes (2: 300 x 2000 x 4160 30.9 against 34.4 us but
-// 256 x 3072 x 12288 36.5 against 35.4; 8: up to 40% slower).  Returns S (1: no split)
-// and sets ks.
+// 256 x 3072 x 12288 36.5 against 35.4; 8: up to 40% slower).  Grids of at most
+// kNvHalfSplitTiles tiles split their 256 x 128 column halves instead (twice the units,
+// half the ranges: less partial traffic per unit of work).
 constexpr int kNvSlots = 256;
 constexpr int kNvMinSplitK = 8;
 constexpr int kNvMinSplitGroups = 4;
+constexpr int kNvHalfSplitTiles = 64;
+// A last round of at most this many tiles runs them as half tiles (see ckh_scaled_mm_nvfp4).
+constexpr int kNvHalfTail = kNvSlots / 2;
 
-int nv_split_count(int64_t M, int64_t N, int64_t K, int& ks) {
-    ks = 0;
-    if (M <= kNvSkinnyMaxM) return 1;
+struct NvSplitPlan {
+    int S = 1;   // K ranges (1: no split)
+    int ks = 0;  // groups per range
+    int nw = 4;  // 4: full tiles, 2: half tiles
+};
+
+NvSplitPlan nv_split_plan(int64_t M, int64_t N, int64_t K) {
+    NvSplitPlan sp;
+    if (M <= kNvSkinnyMaxM) return sp;
     const int tiles = static_cast<int>(cdiv(M, nv::BM) * cdiv(N, nv::BN));
     const int NG = static_cast<int>(cdiv(K / 2, nv::GKB));
-    if (tiles > kNvSlots / 2 || NG < kNvMinSplitK) return 1;
-    const int S = min(kNvSlots / tiles, NG / kNvMinSplitGroups);
-    if (S < 2) return 1;
-    ks = static_cast<int>(cdiv(NG, S));
-    return static_cast<int>(cdiv(NG, ks));
+    if (tiles > kNvSlots / 2 || NG < kNvMinSplitK) return sp;
+    const bool half = tiles <= kNvHalfSplitTiles;
+    const int units = half ? 2 * tiles : tiles;
+    const int S = min(kNvSlots / units, NG / kNvMinSplitGroups);
+    if (S < 2) return sp;
+    sp.ks = static_cast<int>(cdiv(NG, S));
+    sp.S = static_cast<int>(cdiv(NG, sp.ks));
+    sp.nw = half ? 2 : 4;
+    return sp;
 }
 
+// one partial tile (or two partial half tiles) per tile and K range
 int64_t nv_split_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    int ks;
-    const int S = nv_split_count(M, N, K, ks);
-    if (S < 2) return 0;
-    return cdiv(M, nv::BM) * cdiv(N, nv::BN) * S * static_cast<int64_t>(nv::kPartTile) * 4;
+    const NvSplitPlan sp = nv_split_plan(M, N, K);
+    if (sp.S < 2) return 0;
+    return cdiv(M, nv::BM) * cdiv(N, nv::BN) * sp.S * static_cast<int64_t>(nv::kPartTile) * 4;
+}
+
+template <int NW>
+void launch_nv_split(const nv::Args& p, int out_code, int bias_code, bool has_bias, hipStream_t st) {
+    const int units = p.tiles_m * p.tiles_n * (4 / NW);
+    hipLaunchKernelGGL(nv::gemm_split_kernel<NW>, dim3(static_cast<unsigned>(units * p.splits)), dim3(nv::NT), 0, st,
+                       p);
+    const dim3 g2(static_cast<unsigned>(units * (nv::BM * 64 * NW / 4 / 256)));
+#define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_reduce_kernel<O, B, NW>), g2, dim3(256), 0, st, p)
+#define BY_BIAS(O)                                         \
+    do {                                                   \
+        if (!has_bias) LAUNCH(O, -1);                      \
+        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
+        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
+        else LAUNCH(O, CKH_BF16);                          \
+    } while (0)
+    if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
+    else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
+    else BY_BIAS(CKH_F32);
+#undef BY_BIAS
+#undef LAUNCH
 }
 
 int launch_nv_skinny(const nv::Args& q, int out_code, int bias_code, bool has_bias, hipStream_t st) {
@@ -1019,31 +1109,23 @@ extern "C" int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa,
     p.tiles_n = static_cast<int>(cdiv(N, nv::BN));
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (p.M <= kNvSkinnyMaxM) return launch_nv_skinny(p, out_code, bias_code, bias != nullptr, st);
-    int ks;
-    const int S = nv_split_count(M, N, K, ks);
-    if (S > 1 && workspace && workspace_bytes >= nv_split_workspace_bytes(M, N, K)) {
-        p.splits = S;
-        p.ks = ks;
+    const NvSplitPlan sp = nv_split_plan(M, N, K);
+    if (sp.S > 1 && workspace && workspace_bytes >= nv_split_workspace_bytes(M, N, K)) {
+        p.splits = sp.S;
+        p.ks = sp.ks;
         p.part = static_cast<float*>(workspace);
-        const int tiles = p.tiles_m * p.tiles_n;
-        hipLaunchKernelGGL(nv::gemm_split_kernel, dim3(static_cast<unsigned>(tiles * S)), dim3(nv::NT), 0, st, p);
-        const dim3 g2(static_cast<unsigned>(tiles * (nv::kPartTile / 4 / 256)));
-#define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_reduce_kernel<O, B>), g2, dim3(256), 0, st, p)
-#define BY_BIAS(O)                                         \
-    do {                                                   \
-        if (!bias) LAUNCH(O, -1);                          \
-        else if (bias_code == CKH_F32) LAUNCH(O, CKH_F32); \
-        else if (bias_code == CKH_F16) LAUNCH(O, CKH_F16); \
-        else LAUNCH(O, CKH_BF16);                          \
-    } while (0)
-        if (out_code == CKH_BF16) BY_BIAS(CKH_BF16);
-        else if (out_code == CKH_F16) BY_BIAS(CKH_F16);
-        else BY_BIAS(CKH_F32);
-#undef BY_BIAS
-#undef LAUNCH
+        if (sp.nw == 2) launch_nv_split<2>(p, out_code, bias_code, bias != nullptr, st);
+        else launch_nv_split<4>(p, out_code, bias_code, bias != nullptr, st);
         return check_launch("scaled_mm_nvfp4");
     }
-    dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+    // The tiles run one per CU in rounds.  When the last round would be at most half full,
+    // its tiles run as twice as many 256 x 128 half tiles in the same grid (a grid of one
+    // round with no split-K workspace runs all of its tiles so).
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int tail = tiles > kNvSlots ? tiles % kNvSlots : tiles;
+    p.n_half = (tail > 0 && tail <= kNvHalfTail) ? tail : 0;
+    p.n_full = tiles - p.n_half;
+    dim3 grid(static_cast<unsigned>(p.n_full + 2 * p.n_half));
 #define LAUNCH(O, B) hipLaunchKernelGGL((nv::gemm_kernel<O, B>), grid, dim3(nv::NT), 0, st, p)
 #define BY_BIAS(O)                                         \
     do {                                                   \

@@ -387,12 +387,37 @@ def test_scaled_mm_nvfp4_workspace_bytes(hip):
     import comfy_kitchen.backends.hip as hb
 
     f = hb._lib.ckh_scaled_mm_nvfp4_workspace_bytes
-    assert f(256, 13824, 5120) == 54 * 4 * 256 * 256 * 4  # 54 tiles, 20 groups: 4 ranges of 5
-    assert f(256, 5120, 13824) == 20 * 11 * 256 * 256 * 4  # 54 groups: 11 ranges of 5
+    # at most 64 tiles split their column halves: 108 half tiles, 20 groups: 2 ranges of 10
+    assert f(256, 13824, 5120) == 54 * 2 * 256 * 256 * 4
+    assert f(256, 5120, 13824) == 20 * 6 * 256 * 256 * 4  # 40 half tiles, 54 groups: 6 ranges of 9
+    assert f(256, 18432, 8192) == 72 * 3 * 256 * 256 * 4  # 72 whole tiles, 32 groups: 3 ranges of 11
     assert f(8192, 13824, 5120) == 0  # 1728 tiles
     assert f(64, 13824, 5120) == 0  # skinny kernel
     assert f(256, 13824, 1024) == 0  # 4 groups
     assert f(0, 4096, 8192) == 0
+
+
+@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float32, True)])
+def test_scaled_mm_nvfp4_half_tile_tail(out_dtype, with_bias, hip):
+    """289 tiles of 256 x 256: 256 run as full tiles, the last 33 as 66 half-width tiles
+    (partial ones at the right edge, one wholly past N); and a one-round grid without a
+    workspace, all of it half tiles."""
+    m, n, k = 4352, 4196, 320
+    qx, sx, gx, qw, sw, gw = nv_operands(m, n, k, seed=23)
+    bias = (torch.randn(n) * 0.1).float() if with_bias else None
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, bias=bias, out_dtype=torch.float32)
+    got = ck.scaled_mm_nvfp4(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(),
+                             bias=None if bias is None else bias.cuda(), out_dtype=out_dtype)
+    assert got.shape == (m, n) and got.dtype == out_dtype
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
+    # The tiles are taken in groups of 6 tile rows, each group column by column: tiles
+    # 256..288 lie in the last group (tile rows 12..16) at tile columns 10..16.
+    assert rel_l2(got[12 * 256:, 10 * 256:], want[12 * 256:, 10 * 256:]) <= REL_L2[out_dtype]
+    # 3 x 5 tiles, no split (K = 1024: 4 groups), as 30 half tiles
+    qx, sx, gx, qw, sw, gw = nv_operands(700, 1100, 1024, seed=24)
+    want = ref.scaled_mm_nvfp4_ref(qx, qw, gx, gw, sx, sw, out_dtype=torch.float32)
+    got = _nv_abi(qx.cuda(), qw.cuda(), gx.cuda(), gw.cuda(), sx.cuda(), sw.cuda(), out_dtype, None)
+    assert rel_l2(got, want) <= REL_L2[out_dtype]
 
 
 def test_scaled_mm_nvfp4_skinny_matches_tile_rows(hip):
