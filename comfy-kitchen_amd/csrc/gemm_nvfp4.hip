@@ -22,7 +22,10 @@
 // Packed codes and scale words go to LDS unchanged (4x less LDS traffic than fp16
 // tiles) in groups of 4 stages (one 128-byte line per row), double-buffered, by
 // buffer_load_dwordx4 ... lds: 18 direct-to-LDS loads per wave per group, one barrier
-// per group, and a whole group (~8000 MFMA cycles) of latency cover.
+// per group, and a whole group (~8000 MFMA cycles) of latency cover.  A last round of
+// tiles at most half full, and the split-K of a grid of at most 64 tiles, run 256 x 128
+// column halves instead (each wave 128 x 64; the same body with NW = 2 weight tiles per
+// wave): twice the workgroups for the CUs the grid would leave idle.
 //
 // Within a stage each lane needs, per 32-row tile, 16 bytes (32 codes: k = 32h ..
 // 32h+31 of the stage for lane half h, of which MFMA substep kk uses bytes 4kk..4kk+3)

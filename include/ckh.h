@@ -205,7 +205,8 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
 
 /*
  * Bytes of device workspace ckh_scaled_mm_nvfp4 uses at this shape to split K (0: no
- * split): grids of at most 128 output tiles of 256 x 256 with K of at least 2048.  No
+ * split): grids of at most 128 output tiles of 256 x 256 with K of at least 2048 (grids
+ * of at most 64 tiles split as 256 x 128 half tiles).  No
  * counterpart in the reference (its launcher takes a cuBLASLt workspace of the caller's
  * size).
  */
