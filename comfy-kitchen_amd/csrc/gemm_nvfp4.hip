@@ -957,9 +957,16 @@ constexpr int kNvSkinnyMaxM = 64;
 // measured no better than 4 over six shapes (2: 300 x 2000 x 4160 30.9 against 34.4 us but
 // 256 x 3072 x 12288 36.5 against 35.4; 8: up to 40% slower).  Grids of at most
 // kNvHalfSplitTiles tiles split their 256 x 128 column halves instead (twice the units,
-// half the ranges: less partial traffic per unit of work).
+// half the ranges: less partial traffic per unit of work).  Grids of 65-128 tiles split
+// whole tiles only into three ranges or more and from kNvMinSplitKFull groups on; otherwise
+// they run as one round of whole-K half tiles, which write no partials (same process, split
+// against half tiles: two ranges, 256 x 32768 x 5120 86.0 against 73.8 us, 2048 x 4096 x
+// 5376 86.6 against 74.4, 384 x 12288 x 6144 74.3 against 71.8; three ranges of 4 groups,
+// 256 x 18432 x 3072 44.6 against 39.8; three of 11 and 7, 256 x 18432 x 8192 77.4 against
+// 90.9 and 512 x 8704 x 5120 55.7 against 59.5).
 constexpr int kNvSlots = 256;
 constexpr int kNvMinSplitK = 8;
+constexpr int kNvMinSplitKFull = 16;
 constexpr int kNvMinSplitGroups = 4;
 constexpr int kNvHalfSplitTiles = 64;
 // A last round of at most this many tiles runs them as half tiles (see ckh_scaled_mm_nvfp4).
@@ -976,11 +983,11 @@ NvSplitPlan nv_split_plan(int64_t M, int64_t N, int64_t K) {
     if (M <= kNvSkinnyMaxM) return sp;
     const int tiles = static_cast<int>(cdiv(M, nv::BM) * cdiv(N, nv::BN));
     const int NG = static_cast<int>(cdiv(K / 2, nv::GKB));
-    if (tiles > kNvSlots / 2 || NG < kNvMinSplitK) return sp;
     const bool half = tiles <= kNvHalfSplitTiles;
+    if (tiles > kNvSlots / 2 || NG < (half ? kNvMinSplitK : kNvMinSplitKFull)) return sp;
     const int units = half ? 2 * tiles : tiles;
     const int S = min(kNvSlots / units, NG / kNvMinSplitGroups);
-    if (S < 2) return sp;
+    if (S < (half ? 2 : 3)) return sp;
     sp.ks = static_cast<int>(cdiv(NG, S));
     sp.S = static_cast<int>(cdiv(NG, sp.ks));
     sp.nw = half ? 2 : 4;

@@ -205,8 +205,9 @@ int ckh_scaled_mm_nvfp4(const void* a, const void* b, const void* sa, const void
 
 /*
  * Bytes of device workspace ckh_scaled_mm_nvfp4 uses at this shape to split K (0: no
- * split): grids of at most 128 output tiles of 256 x 256 with K of at least 2048 (grids
- * of at most 64 tiles split as 256 x 128 half tiles).  No
+ * split): grids of at most 64 output tiles of 256 x 256 with K of at least 2048 (split as
+ * 256 x 128 half tiles), and grids of 65-128 tiles with K of at least 4096 when three K
+ * ranges or more fit.  No
  * counterpart in the reference (its launcher takes a cuBLASLt workspace of the caller's
  * size).
  */

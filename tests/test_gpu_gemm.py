@@ -359,9 +359,11 @@ def _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias=None):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("m,n,k", [(256, 4096, 2048), (300, 2000, 4160), (129, 520, 5152), (65, 13824, 2048)])
+@pytest.mark.parametrize("m,n,k", [(256, 4096, 2048), (300, 2000, 4160), (129, 520, 5152), (65, 13824, 2048),
+                                   (300, 8500, 4096)])
 def test_scaled_mm_nvfp4_split_k(m, n, k, out_dtype, hip):
-    """Small NVFP4 tile grids split K into a workspace (ranges of ks 256-element groups, odd
+    """Small NVFP4 tile grids split K into a workspace, as half tiles (at most 64 tiles) or
+    whole tiles (300 x 8500: 68 tiles, 3 ranges) (ranges of ks 256-element groups, odd
     counts and odd starts included, and a last range shorter than the others, down to one
     group; K % 256 != 0, rows past M, columns past N), against the oracle and against the
     unsplit call (fp32 summation order only; an odd group count there too); the reduce
@@ -391,6 +393,8 @@ def test_scaled_mm_nvfp4_workspace_bytes(hip):
     assert f(256, 13824, 5120) == 54 * 2 * 256 * 256 * 4
     assert f(256, 5120, 13824) == 20 * 6 * 256 * 256 * 4  # 40 half tiles, 54 groups: 6 ranges of 9
     assert f(256, 18432, 8192) == 72 * 3 * 256 * 256 * 4  # 72 whole tiles, 32 groups: 3 ranges of 11
+    assert f(256, 32768, 5120) == 0  # 128 tiles: only 2 ranges fit, whole-K half tiles instead
+    assert f(256, 18432, 3072) == 0  # 72 tiles, 12 groups: whole tiles split from 16 groups on
     assert f(8192, 13824, 5120) == 0  # 1728 tiles
     assert f(64, 13824, 5120) == 0  # skinny kernel
     assert f(256, 13824, 1024) == 0  # 4 groups
