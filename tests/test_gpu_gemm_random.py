@@ -4,7 +4,8 @@ The GEMM launchers choose among many forms by M, N and K: skinny kernels (waves,
 tiles and staged activation rows by M and N), whole tiles, half tiles for a last or only
 round, weight-prefetch workgroups on idle CUs, and split-K in full or half tiles with
 ranges of any length.  Each case draws a shape from ranges that straddle those choices, so
-the suite crosses their boundaries in combinations the hand-picked shapes do not.
+the suite crosses their boundaries in combinations the hand-picked shapes do not; a few
+larger grids with short K cover the whole-tile rounds and their last rounds.
 """
 import random
 
@@ -35,7 +36,14 @@ def _shapes(seed: int, count: int):
     return out
 
 
-@pytest.mark.parametrize("m,n,k", _shapes(2024, 24))
+def _big_shapes(seed: int, count: int):
+    """Grids of 72-378 tiles of 256 x 256 (one round of whole tiles, or several rounds and
+    a last round of full or half tiles), with short K to keep the oracle fast."""
+    rng = random.Random(seed)
+    return [(rng.randint(1500, 4600), rng.randint(3000, 5200), 32 * rng.randint(1, 10)) for _ in range(count)]
+
+
+@pytest.mark.parametrize("m,n,k", _shapes(2024, 24) + _big_shapes(77, 6))
 def test_scaled_mm_mxfp8_random_shapes(m, n, k, hip):
     g = torch.Generator().manual_seed(m * 131 + n * 7 + k)
     x = (torch.randn(m, k, generator=g) * torch.exp(torch.randn(m, 1, generator=g))).bfloat16()
@@ -54,7 +62,7 @@ def test_scaled_mm_mxfp8_random_shapes(m, n, k, hip):
     assert rel_l2(got8, want8) <= REL_L2[out_dtype]
 
 
-@pytest.mark.parametrize("m,n,k", _shapes(4048, 24))
+@pytest.mark.parametrize("m,n,k", _shapes(4048, 24) + _big_shapes(78, 6))
 def test_scaled_mm_nvfp4_random_shapes(m, n, k, hip):
     g = torch.Generator().manual_seed(m * 137 + n * 11 + k)
     x = torch.randn(m, k, generator=g).bfloat16()
