@@ -952,18 +952,20 @@ constexpr int kNvSkinnyMaxM = 64;
 // 4 us of MFMA time per tile and a partial tile's round trip about as much as one group.
 // Ranges of an odd number of groups end mid-pair (measured against ranges rounded up to an
 // even count, same process: M = 256, N = 13824, K = 5120, four ranges of 5 instead of 6, 6,
-// 6, 2: 48.7 against 53.8 us; M = 300, N = 2000, K = 4160 35.0 against 39.6; M = 2048,
-// N = 4096, K = 5376 84.6 against 90.1).  Minimum range lengths of 2, 3, 6 and 8 groups
+// 6, 2: 48.7 against 53.8 us; M = 300, N = 2000, K = 4160 35.0 against 39.6; M = 2048, N =
+// 4096, K = 5376 84.6 against 90.1).  Minimum range lengths of 2, 3, 6 and 8 groups
 // measured no better than 4 over six shapes (2: 300 x 2000 x 4160 30.9 against 34.4 us but
 // 256 x 3072 x 12288 36.5 against 35.4; 8: up to 40% slower).  Grids of at most
 // kNvHalfSplitTiles tiles split their 256 x 128 column halves instead (twice the units,
-// half the ranges: less partial traffic per unit of work).  Grids of 65-128 tiles split
-// whole tiles only into three ranges or more and from kNvMinSplitKFull groups on; otherwise
-// they run as one round of whole-K half tiles, which write no partials (same process, split
-// against half tiles: two ranges, 256 x 32768 x 5120 86.0 against 73.8 us, 2048 x 4096 x
-// 5376 86.6 against 74.4, 384 x 12288 x 6144 74.3 against 71.8; three ranges of 4 groups,
-// 256 x 18432 x 3072 44.6 against 39.8; three of 11 and 7, 256 x 18432 x 8192 77.4 against
-// 90.9 and 512 x 8704 x 5120 55.7 against 59.5).
+// half the ranges: less partial traffic per unit of work), also in ranges of at least
+// kNvMinSplitGroups (3 measured 2-4% faster on three shapes but 16% slower on 512 x 3072 x
+// 3072; 2 slower on four of five).  Grids of 65-128 tiles split whole tiles only into three
+// ranges or more and from kNvMinSplitKFull groups on; otherwise they run as one round of
+// whole-K half tiles, which write no partials (same process, split against half tiles: two
+// ranges, 256 x 32768 x 5120 86.0 against 73.8 us, 2048 x 4096 x 5376 86.6 against 74.4,
+// 384 x 12288 x 6144 74.3 against 71.8; three ranges of 4 groups, 256 x 18432 x 3072 44.6
+// against 39.8; three of 11 and 7, 256 x 18432 x 8192 77.4 against 90.9 and 512 x 8704 x
+// 5120 55.7 against 59.5).
 constexpr int kNvSlots = 256;
 constexpr int kNvMinSplitK = 8;
 constexpr int kNvMinSplitKFull = 16;
