@@ -84,7 +84,7 @@ def test_scaled_mm_mxfp8_extreme_scales(hip):
     assert d.abs().max().item() <= 5e-4
 
 
-@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float32, True)])
+@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float16, True), (torch.float32, True)])
 def test_scaled_mm_mxfp8_half_tile_tail(out_dtype, with_bias, hip):
     """289 tiles of 256 x 256: 256 run as full tiles, the last 33 as 66 half-width tiles
     (partial ones at the right edge, one wholly past N)."""
@@ -178,7 +178,7 @@ def _mx_abi(qx, qw, sx, sw, out_dtype, ws):
     return out
 
 
-@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(256, 4096, 4096), (300, 2000, 4160), (129, 520, 4128), (65, 18432, 4096),
                                    (512, 3072, 13824), (200, 2000, 2080)])
 def test_scaled_mm_mxfp8_split_k(m, n, k, out_dtype, hip):
@@ -358,7 +358,7 @@ def _nv_abi(qx, qw, gx, gw, sx, sw, out_dtype, ws, bias=None):
     return out
 
 
-@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("m,n,k", [(256, 4096, 2048), (300, 2000, 4160), (129, 520, 5152), (65, 13824, 2048),
                                    (300, 8500, 4096)])
 def test_scaled_mm_nvfp4_split_k(m, n, k, out_dtype, hip):
@@ -401,7 +401,7 @@ def test_scaled_mm_nvfp4_workspace_bytes(hip):
     assert f(0, 4096, 8192) == 0
 
 
-@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float32, True)])
+@pytest.mark.parametrize("out_dtype,with_bias", [(torch.bfloat16, False), (torch.float16, True), (torch.float32, True)])
 def test_scaled_mm_nvfp4_half_tile_tail(out_dtype, with_bias, hip):
     """289 tiles of 256 x 256: 256 run as full tiles, the last 33 as 66 half-width tiles
     (partial ones at the right edge, one wholly past N); and a one-round grid without a
