@@ -7,6 +7,8 @@ backends/eager/__init__.py:118-131): bit-exact with 16-bit freqs; with fp32 freq
 2^-21 of the sum of the two product magnitudes (the kernel adds the second product with
 one rounding, eager with two).
 """
+import random
+
 import pytest
 import torch
 
@@ -128,3 +130,29 @@ def test_fp32_x(freqs_dtype, shape, hip, seed):
         mag = (fd[..., 0] * xp[..., 0]).abs() + (fd[..., 1] * xp[..., 1]).abs()
         err = (g.double() - w.double()).reshape(mag.shape).abs()
         assert bool((err <= mag * 2.0 ** -21 + 1e-38).all()), float((err / mag.clamp_min(1e-30)).max())
+
+
+def _random_cases(seed: int, count: int):
+    """(b, h, n, d, per-batch freqs, per-head freqs, x dtype, freqs dtype, seed)"""
+    rng = random.Random(seed)
+    return [(rng.randint(1, 3), rng.randint(1, 24), rng.randint(1, 600), rng.choice([6, 8, 16, 32, 48, 64, 96, 128, 256]),
+             rng.random() < 0.3, rng.random() < 0.2, rng.choice(["bf16", "f16"]), rng.choice(["f32", "f16", "bf16"]),
+             rng.randrange(1 << 30)) for _ in range(count)]
+
+
+_DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+@pytest.mark.parametrize("b,h,n,d,fb,fh,xdt,fdt,seed", _random_cases(7, 24))
+def test_random_shapes(b, h, n, d, fb, fh, xdt, fdt, seed, hip):
+    """Seeded random batch, heads, positions, head_dim (vector and scalar paths) and freqs
+    broadcast over batch and heads or not, through both ops."""
+    g = torch.Generator().manual_seed(seed)
+    f = torch.randn(b if fb else 1, h if fh else 1, n, d // 2, 2, 2, generator=g).to(_DT[fdt])
+    xq = torch.randn(b, h, n, d, generator=g).to(_DT[xdt])
+    xk = torch.randn(b, h, n, d, generator=g).to(_DT[xdt])
+    wq, wk = ref.apply_rope(xq, xk, f)
+    gq, gk = ck.apply_rope(xq.cuda(), xk.cuda(), f.cuda())
+    check(gq, wq)
+    check(gk, wk)
+    assert torch.equal(ck.apply_rope1(xq.cuda(), f.cuda()).cpu(), gq.cpu())
